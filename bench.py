@@ -1,0 +1,216 @@
+"""Benchmark of the stride-aware elementwise + reduction path on one MI355X.
+
+Metric: achieved HBM GB/s, and the fraction of MI355X's 8 TB/s peak, for
+f32 add, axis-sum and argmax.  One step = one pass of the hot path over the BASELINE configs
+that metric names:
+    C1  add      f32, 16,777,216 elements U(-1,1), seed 0            12 B/elem
+    C4  sum      axis=-1 of an (8192, 8192) f32 N(0,1) array, seed 0   4 B/elem + 4 B/row
+    C4  argmax   axis=1 of the same array -> int64                    4 B/elem + 8 B/row
+Inputs are resident in HBM before timing.  Each launch is bracketed by HIP events on the
+stream it runs on, and a 1 GiB write is issued before every launch (outside the events) so the
+256 MB Infinity Cache cannot serve the inputs.  `value` = algorithmic bytes of the step /
+summed kernel time.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
+musapy's CPU path) on the same step.
+
+    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--all", action="store_true", help="also time every BASELINE config (table on stderr)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-flush", action="store_true", help="do not evict the Infinity Cache between launches")
+    return p.parse_args()
+
+
+class Bench:
+    def __init__(self, ms, flush=True):
+        self.ms = ms
+        self.flush_buf = ms.from_numpy(np.zeros(1 << 28, np.float32)) if flush else None  # 1 GiB
+        self.timer = ms._core._Timer(0)
+
+    def flush(self):
+        if self.flush_buf is not None:
+            self.ms._core._fill_u32(self.flush_buf, 0x3F800000)
+
+    def time_op(self, fn, reps):
+        """Average kernel time (ms) of fn() over reps launches, each after a cache flush."""
+        total = 0.0
+        out = None
+        for _ in range(reps):
+            self.flush()
+            self.timer.start()
+            out = fn()
+            self.timer.stop()
+            total += self.timer.elapsed_ms()
+        return total / reps, out
+
+
+def step_ops(ms):
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, 16_777_216).astype(np.float32)
+    b = rng.uniform(-1, 1, 16_777_216).astype(np.float32)
+    x = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
+    A, B, X = ms.from_numpy(a), ms.from_numpy(b), ms.from_numpy(x)
+    n = 8192 * 8192
+    ops = [
+        ("C1 add f32 16,777,216", lambda: ms.add(A, B), 12 * 16_777_216),
+        ("C4 sum axis=-1 (8192,8192) f32", lambda: ms.sum(X, axis=-1), 4 * n + 4 * 8192),
+        ("C4 argmax axis=1 (8192,8192) f32", lambda: ms.argmax(X, axis=1), 4 * n + 8 * 8192),
+    ]
+    host = {"a": a, "b": b, "x": x}
+    return ops, host
+
+
+def all_config_ops(ms):
+    """Every BASELINE config op (for the per-config table)."""
+    rng = np.random.default_rng(0)
+    ops = []
+    a64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
+    b64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
+    A64, B64 = ms.from_numpy(a64), ms.from_numpy(b64)
+    ops.append(("C1-64M add f32 67,108,864", lambda: ms.add(A64, B64), 12 * 67_108_864))
+    ops.append(("full sum f32 64M", lambda: ms.sum(A64), 4 * 67_108_864 + 4))
+    ops.append(("full argmax f32 64M", lambda: ms.argmax(A64), 4 * 67_108_864 + 8))
+    r = np.random.default_rng(0)
+    ca = ms.from_numpy(r.uniform(-1, 1, (4096, 1)).astype(np.float32))
+    cb = ms.from_numpy(r.uniform(-1, 1, (8192,)).astype(np.float32))
+    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda: ms.add(ca, cb), 4 * 33_554_432 + 4 * 4096 + 4 * 8192))
+    xt = ms.transpose(ms.from_numpy(np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32)))
+    ops.append(("C2 exp transposed (8192,4096)^T", lambda: ms.exp(xt), 8 * 33_554_432))
+    r = np.random.default_rng(0)
+    i64 = ms.from_numpy(r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64))
+    f64 = ms.from_numpy(r.standard_normal((2048, 2048, 4)))
+    N = 16_777_216
+    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda: ms.add(i64, f64), 24 * N))
+    s = ms.add(i64, f64)
+    ops.append(("C3 clamp f64", lambda: ms.clamp(s, -1.0, 1.0), 16 * N))
+    c = ms.clamp(s, -1.0, 1.0)
+    ops.append(("C3 astype f64->f32", lambda: ms.astype(c, "f32"), 12 * N))
+    f = ms.astype(c, "f32")
+    ops.append(("C3 astype f32->bf16", lambda: ms.astype(f, "bf16"), 6 * N))
+    ops.append(("C3 astype f32->f16", lambda: ms.astype(f, "f16"), 6 * N))
+    X = ms.from_numpy(np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32))
+    n = 8192 * 8192
+    ops.append(("C4 sum axis=0", lambda: ms.sum(X, axis=0), 4 * n + 4 * 8192))
+    ops.append(("C4 mean axis=-1", lambda: ms.mean(X, axis=-1), 4 * n + 4 * 8192))
+    ops.append(("C4 mean axis=0", lambda: ms.mean(X, axis=0), 4 * n + 4 * 8192))
+    ops.append(("C4 max axis=(0,1)", lambda: ms.max(X, axis=(0, 1)), 4 * n + 4))
+    ops.append(("C4 argmin axis=1", lambda: ms.argmin(X, axis=1), 4 * n + 8 * 8192))
+    y = ms.from_numpy(np.random.default_rng(0).random((1024, 65536)))
+    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda: ms.cumsum(y, axis=1), 16 * 1024 * 65536))
+    r = np.random.default_rng(0)
+    z = (r.standard_normal((16, 1024, 1024), dtype=np.float32)
+         + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
+    Z = ms.from_numpy(z)
+    ops.append(("C5 c64 sum axis=(1,2)", lambda: ms.sum(Z, axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128))
+    return ops
+
+
+def cpu_baseline(host):
+    """The CPU oracle (single thread) on the same step; returns (GB/s, seconds, sample)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import reference as R
+
+    n = 8192 * 8192
+    algo = 12 * 16_777_216 + (4 * n + 4 * 8192) + (4 * n + 8 * 8192)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        R.binary("add", host["a"], host["b"])
+        R.reduce(host["x"], "sum", -1)
+        R.reduce(host["x"], "argmax", 1)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 8.0 or reps >= 10:
+            break
+    return algo * reps / el / 1e9, el / reps, f"the full step (C1 add 16M + C4 sum axis=-1 + C4 argmax axis=1), {reps} passes"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards with no "
+              f"exchange (see DESIGN.md) and this build runs on single-GPU boxes.", file=sys.stderr)
+        sys.exit(2)
+    import musapy_amd as ms
+
+    b = Bench(ms, flush=not args.no_flush)
+    ops, host = step_ops(ms)
+    for name, fn, _ in ops:  # warm-up (first launch loads code objects)
+        for _ in range(max(args.warmup, 1)):
+            fn()
+    ms.synchronize()
+    per_op = {}
+    t0 = time.perf_counter()
+    ms.synchronize()
+    for _ in range(args.steps):
+        for name, fn, bytes_ in ops:
+            t, _ = b.time_op(fn, 1)
+            per_op.setdefault(name, []).append(t)
+    ms.synchronize()
+    wall = time.perf_counter() - t0
+    table = {}
+    total_bytes, total_ms = 0, 0.0
+    for name, fn, bytes_ in ops:
+        t = float(np.mean(per_op[name]))
+        table[name] = {"ms": round(t, 5), "algo_bytes": bytes_, "GBps": round(bytes_ / t / 1e6, 1),
+                       "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4)}
+        total_bytes += bytes_
+        total_ms += t
+    dom = max(table, key=lambda k: table[k]["ms"])
+    value = total_bytes / total_ms / 1e6
+    line = {
+        "metric": "achieved HBM GB/s (and % of MI355X peak) for f32 add, axis-sum, argmax",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms, 5),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy default_rng seed 0, BASELINE.json C1/C4 distributions)",
+        "config": {"workload": "C1 add f32 16,777,216 + C4 sum axis=-1 + C4 argmax axis=1 on (8192,8192) f32",
+                   "parallelism": "single GPU"},
+        "frac_of_peak": round(value / PEAK_GBS, 4),
+        "ops": table,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["GBps"], "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": None},
+    }
+    if not args.no_cpu:
+        v, sec, sample = cpu_baseline(host)
+        line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                                "sample": sample, "seconds_per_pass": round(sec, 3)}
+    if args.all:
+        rows = []
+        for name, fn, bytes_ in all_config_ops(ms):
+            fn()
+            t, _ = b.time_op(fn, 5)
+            rows.append({"op": name, "ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
+                         "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4)})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        line["all_configs"] = rows
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

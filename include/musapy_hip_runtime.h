@@ -1,0 +1,68 @@
+/*
+ * musapy_hip_runtime.h -- thin C-ABI HIP runtime layer under the op layer.
+ *
+ * Replaces the MUSA runtime bindings and the memory/stream plumbing of musapy-core:
+ *   rust/musapy-core/src/musa_ffi.rs:25-150      musaMalloc/Free/Memcpy/Stream/Event bindings
+ *   rust/musapy-core/src/musa_ffi.rs:369-408     check_musa / check_last_kernel_launch
+ *   rust/musapy-core/src/buffer_pool.rs:51-170    size-class cache of device buffers
+ *   rust/musapy-core/src/deferred_free.rs:55-138  free-after-sync queue
+ *   rust/musapy-core/src/mem_stats.rs:18-114      allocation counters
+ * Device memory comes from hipMallocAsync on the device's default memory pool with an unlimited
+ * release threshold: frees are stream-ordered (no deferred-free queue is needed) and freed
+ * blocks are recycled by the pool.  All functions return 0 on success or a hipError_t code.
+ * Streams are always created with the default priority.
+ */
+#ifndef MUSAPY_HIP_RUNTIME_H
+#define MUSAPY_HIP_RUNTIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+typedef struct ihipStream_t* hipStream_t;
+typedef struct ihipEvent_t* hipEvent_t;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int mpy_rt_device_count(int* count);
+int mpy_rt_set_device(int device);
+/* name / total HBM bytes / CU count / peak memory clock of a device */
+int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_mem, int* cu_count, int* arch_major,
+                       int* arch_minor);
+
+/* stream-ordered allocation on `device` (pool-backed); `stream` may be NULL (null stream) */
+int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream);
+int mpy_rt_free(void* ptr, hipStream_t stream);
+
+int mpy_rt_memcpy_h2d(void* dst, const void* src, size_t nbytes, hipStream_t stream);
+int mpy_rt_memcpy_d2h(void* dst, const void* src, size_t nbytes, hipStream_t stream);
+int mpy_rt_memcpy_d2d(void* dst, const void* src, size_t nbytes, hipStream_t stream);
+
+int mpy_rt_stream_create(hipStream_t* stream, int device);
+int mpy_rt_stream_destroy(hipStream_t stream);
+int mpy_rt_stream_synchronize(hipStream_t stream);
+int mpy_rt_device_synchronize(void);
+
+int mpy_rt_event_create(hipEvent_t* event, int timing);
+int mpy_rt_event_destroy(hipEvent_t event);
+int mpy_rt_event_record(hipEvent_t event, hipStream_t stream);
+int mpy_rt_stream_wait_event(hipStream_t stream, hipEvent_t event);
+int mpy_rt_event_synchronize(hipEvent_t event);
+int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop);
+
+/* After a kernel-ABI call: returns the pending launch error (hipGetLastError) or, if none, the
+ * kernel library's own wrapper error (musapy_kernels_take_error, mapped to -1). */
+int mpy_rt_check_launch(void);
+const char* mpy_rt_error_string(int code);
+
+/* allocation statistics of this process: live bytes, high-water mark, allocation count */
+void mpy_rt_mem_stats(size_t* live_bytes, size_t* peak_bytes, size_t* num_allocs);
+
+/* Writes `nbytes` of a pattern to `ptr` with a kernel (graph-capture safe, unlike memset). */
+int mpy_rt_fill_u32(void* ptr, uint32_t value, size_t nbytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MUSAPY_HIP_RUNTIME_H */

@@ -1,0 +1,264 @@
+/*
+ * musapy_kernels.h -- C ABI of the MI355X (gfx950) elementwise / reduction / scan kernels.
+ *
+ * This is the drop-in boundary for musapy's stride-aware hot path.  Every symbol below has the
+ * exact name and argument list that musapy's Rust op layer binds in
+ * rust/musapy-ops/src/kernels.rs (the `unsafe extern "C"` block, lines 16-346); the line of
+ * kernels.rs each declaration replaces is given beside it.  `musaStream_t` becomes `hipStream_t`
+ * (both are opaque pointers), `muComplex`/`muDoubleComplex` become musapy_c64_t/musapy_c128_t
+ * (same #[repr(C)] {re, im} layout, rust/musapy-core/src/musa_x_ffi.rs:74-89).
+ *
+ * Conventions (rust/musapy-ops/src/kernels.rs:6-9, docs/adr/ADR.md L2-2):
+ *  - functions return void and never allocate; launch errors are read with hipGetLastError()
+ *    right after the call, execution errors surface at stream synchronisation;
+ *  - data pointers are device pointers already advanced by the view offset;
+ *  - `shape` / `*_strides` are HOST arrays (elements, strides may be 0 or negative) that are only
+ *    read during the call; the output is always C-contiguous and never aliases an input;
+ *  - all launches are asynchronous on `stream`.
+ * Reduction partial/final/mid contract (rust/musapy-ops/src/op_builder.rs:2239-2301,2523):
+ *  partials are laid out [out_size][tiles_per_output]; tile t of output o covers the axis range
+ *  [t*ceil(axis_len/tiles), (t+1)*ceil(axis_len/tiles)); any tiles_per_output >= 1 is accepted.
+ */
+#ifndef MUSAPY_KERNELS_H
+#define MUSAPY_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <sys/types.h>
+
+/* same typedef as <hip/hip_runtime_api.h>; repeating an identical typedef is valid C11/C++ */
+typedef struct ihipStream_t* hipStream_t;
+
+#define MUSAPY_KERNELS_ABI_VERSION 2
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* interleaved complex element, layout-identical to muComplex / muDoubleComplex */
+typedef struct { float re; float im; } musapy_c64_t;
+typedef struct { double re; double im; } musapy_c128_t;
+
+
+/* ---- binary elementwise over broadcast strides ---- */
+/* kernels.rs:19 */ void musapy_add_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:20 */ void musapy_add_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:21 */ void musapy_sub_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:22 */ void musapy_sub_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:23 */ void musapy_mul_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:24 */ void musapy_mul_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:25 */ void musapy_div_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:26 */ void musapy_div_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:27 */ void musapy_pow_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:28 */ void musapy_pow_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+
+/* ---- unary elementwise ---- */
+/* kernels.rs:31 */ void musapy_sin_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:32 */ void musapy_sin_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:33 */ void musapy_cos_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:34 */ void musapy_cos_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:35 */ void musapy_exp_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:36 */ void musapy_exp_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:37 */ void musapy_log_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:38 */ void musapy_log_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:39 */ void musapy_abs_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:40 */ void musapy_abs_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:41 */ void musapy_sign_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:42 */ void musapy_sign_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:43 */ void musapy_neg_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:44 */ void musapy_neg_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+
+/* ---- clamp ---- */
+/* kernels.rs:47 */ void musapy_clamp_f32_v2(const float* a, float* c, float lo, float hi, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:48 */ void musapy_clamp_f64_v2(const double* a, double* c, double lo, double hi, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+
+/* ---- cast (Rust `as` semantics: RNE to float, saturating float->int, NaN->0) ---- */
+/* kernels.rs:51 */ void musapy_cast_i8_f32_v2(const int8_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:52 */ void musapy_cast_i16_f32_v2(const int16_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:53 */ void musapy_cast_i32_f32_v2(const int* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:54 */ void musapy_cast_i64_f32_v2(const int64_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:55 */ void musapy_cast_u8_f32_v2(const uint8_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:56 */ void musapy_cast_u16_f32_v2(const uint16_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:57 */ void musapy_cast_u32_f32_v2(const uint32_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:58 */ void musapy_cast_u64_f32_v2(const uint64_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:59 */ void musapy_cast_f64_f32_v2(const double* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:62 */ void musapy_cast_i8_f64_v2(const int8_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:63 */ void musapy_cast_i16_f64_v2(const int16_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:64 */ void musapy_cast_i32_f64_v2(const int* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:65 */ void musapy_cast_i64_f64_v2(const int64_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:66 */ void musapy_cast_u8_f64_v2(const uint8_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:67 */ void musapy_cast_u16_f64_v2(const uint16_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:68 */ void musapy_cast_u32_f64_v2(const uint32_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:69 */ void musapy_cast_u64_f64_v2(const uint64_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:70 */ void musapy_cast_f32_f64_v2(const float* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:73 */ void musapy_cast_i8_i64_v2(const int8_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:74 */ void musapy_cast_i16_i64_v2(const int16_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:75 */ void musapy_cast_i32_i64_v2(const int* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:76 */ void musapy_cast_u8_i64_v2(const uint8_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:77 */ void musapy_cast_u16_i64_v2(const uint16_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:78 */ void musapy_cast_u32_i64_v2(const uint32_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:79 */ void musapy_cast_u64_i64_v2(const uint64_t* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:80 */ void musapy_cast_f32_i64_v2(const float* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:81 */ void musapy_cast_f64_i64_v2(const double* a, int64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+
+/* New in this backend (no counterpart in kernels.rs: musapy rejects f16/bf16 casts in
+ * validate_cast_pair, rust/musapy-ops/src/op_builder.rs:928-945).  Output is the raw
+ * IEEE binary16 / bfloat16 bit pattern, round-to-nearest-even; NaN stays NaN with its sign
+ * and leading payload bits and the quiet bit set; overflow rounds to +-inf. */
+void musapy_cast_f32_bf16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+
+/* ---- reduction (single pass) ---- */
+/* kernels.rs:139 */ void musapy_sum_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:140 */ void musapy_sum_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:141 */ void musapy_sum_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:142 */ void musapy_prod_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:143 */ void musapy_prod_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:144 */ void musapy_prod_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:145 */ void musapy_max_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:146 */ void musapy_max_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:147 */ void musapy_max_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:148 */ void musapy_min_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:149 */ void musapy_min_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:150 */ void musapy_min_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:151 */ void musapy_mean_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:152 */ void musapy_mean_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:154 */ void musapy_sum_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:155 */ void musapy_sum_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:156 */ void musapy_prod_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:157 */ void musapy_prod_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:158 */ void musapy_mean_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:159 */ void musapy_mean_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+
+/* ---- small-axis reduction (group_size is a hint) ---- */
+/* kernels.rs:161 */ void musapy_sum_small_axis_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:162 */ void musapy_sum_small_axis_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:163 */ void musapy_sum_small_axis_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:164 */ void musapy_prod_small_axis_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:165 */ void musapy_prod_small_axis_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:166 */ void musapy_prod_small_axis_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:167 */ void musapy_max_small_axis_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:168 */ void musapy_max_small_axis_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:169 */ void musapy_max_small_axis_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:170 */ void musapy_min_small_axis_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:171 */ void musapy_min_small_axis_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:172 */ void musapy_min_small_axis_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:173 */ void musapy_mean_small_axis_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:174 */ void musapy_mean_small_axis_f64_v2(const double* a, double* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+
+/* ---- arg reduction (single pass) ---- */
+/* kernels.rs:175 */ void musapy_argmax_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:176 */ void musapy_argmax_f32_v2(const float* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:177 */ void musapy_argmax_f64_v2(const double* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:178 */ void musapy_argmin_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:179 */ void musapy_argmin_f32_v2(const float* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:180 */ void musapy_argmin_f64_v2(const double* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+
+/* ---- cumsum (inclusive scan along one axis; tmp = caller scratch of num_rows*(bpr [+ceil(bpr/256) if bpr>256]) elements, bpr=ceil(axis_len/256), may be NULL when bpr<=1) ---- */
+/* kernels.rs:185 */ void musapy_cumsum_i64_v3(const int64_t* a, int64_t* c, int64_t* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:186 */ void musapy_cumsum_f32_v3(const float* a, float* c, float* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+/* kernels.rs:187 */ void musapy_cumsum_f64_v3(const double* a, double* c, double* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
+
+/* ---- reduction partial ---- */
+/* kernels.rs:222 */ void musapy_sum_partial_i64_v2(const int64_t* a, int64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:223 */ void musapy_sum_partial_f32_v2(const float* a, float* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:224 */ void musapy_sum_partial_f64_v2(const double* a, double* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:225 */ void musapy_prod_partial_i64_v2(const int64_t* a, int64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:226 */ void musapy_prod_partial_f32_v2(const float* a, float* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:227 */ void musapy_prod_partial_f64_v2(const double* a, double* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:228 */ void musapy_max_partial_i64_v2(const int64_t* a, int64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:229 */ void musapy_max_partial_f32_v2(const float* a, float* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:230 */ void musapy_max_partial_f64_v2(const double* a, double* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:231 */ void musapy_min_partial_i64_v2(const int64_t* a, int64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:232 */ void musapy_min_partial_f32_v2(const float* a, float* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:233 */ void musapy_min_partial_f64_v2(const double* a, double* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:235 */ void musapy_mean_partial_f32_v2(const float* a, float* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:236 */ void musapy_mean_partial_f64_v2(const double* a, double* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+
+/* ---- reduction final ---- */
+/* kernels.rs:240 */ void musapy_sum_final_i64_v2(const int64_t* partials, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:241 */ void musapy_sum_final_f32_v2(const float* partials, float* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:242 */ void musapy_sum_final_f64_v2(const double* partials, double* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:243 */ void musapy_prod_final_i64_v2(const int64_t* partials, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:244 */ void musapy_prod_final_f32_v2(const float* partials, float* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:245 */ void musapy_prod_final_f64_v2(const double* partials, double* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:246 */ void musapy_max_final_i64_v2(const int64_t* partials, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:247 */ void musapy_max_final_f32_v2(const float* partials, float* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:248 */ void musapy_max_final_f64_v2(const double* partials, double* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:249 */ void musapy_min_final_i64_v2(const int64_t* partials, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:250 */ void musapy_min_final_f32_v2(const float* partials, float* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:251 */ void musapy_min_final_f64_v2(const double* partials, double* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:254 */ void musapy_mean_final_f32_v2(const float* partials, float* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:255 */ void musapy_mean_final_f64_v2(const double* partials, double* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+
+/* ---- small-axis reduction (group_size is a hint) ---- */
+/* kernels.rs:259 */ void musapy_sum_small_axis_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:260 */ void musapy_sum_small_axis_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:261 */ void musapy_prod_small_axis_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:262 */ void musapy_prod_small_axis_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:263 */ void musapy_mean_small_axis_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+/* kernels.rs:264 */ void musapy_mean_small_axis_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, int group_size, hipStream_t stream);
+
+/* ---- reduction partial ---- */
+/* kernels.rs:265 */ void musapy_sum_partial_c64_v2(const musapy_c64_t* a, musapy_c64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:266 */ void musapy_sum_partial_c128_v2(const musapy_c128_t* a, musapy_c128_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:267 */ void musapy_prod_partial_c64_v2(const musapy_c64_t* a, musapy_c64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:268 */ void musapy_prod_partial_c128_v2(const musapy_c128_t* a, musapy_c128_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:269 */ void musapy_mean_partial_c64_v2(const musapy_c64_t* a, musapy_c64_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:270 */ void musapy_mean_partial_c128_v2(const musapy_c128_t* a, musapy_c128_t* partials, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+
+/* ---- reduction final ---- */
+/* kernels.rs:271 */ void musapy_sum_final_c64_v2(const musapy_c64_t* partials, musapy_c64_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:272 */ void musapy_sum_final_c128_v2(const musapy_c128_t* partials, musapy_c128_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:273 */ void musapy_prod_final_c64_v2(const musapy_c64_t* partials, musapy_c64_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:274 */ void musapy_prod_final_c128_v2(const musapy_c128_t* partials, musapy_c128_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:275 */ void musapy_mean_final_c64_v2(const musapy_c64_t* partials, musapy_c64_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+/* kernels.rs:276 */ void musapy_mean_final_c128_v2(const musapy_c128_t* partials, musapy_c128_t* c, size_t num_partials, size_t out_size, size_t axis_len, hipStream_t stream);
+
+/* ---- reduction partial ---- */
+/* kernels.rs:280 */ void musapy_argmax_partial_i64_v2(const int64_t* a, int64_t* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:281 */ void musapy_argmax_partial_f32_v2(const float* a, float* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:282 */ void musapy_argmax_partial_f64_v2(const double* a, double* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:283 */ void musapy_argmin_partial_i64_v2(const int64_t* a, int64_t* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:284 */ void musapy_argmin_partial_f32_v2(const float* a, float* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+/* kernels.rs:285 */ void musapy_argmin_partial_f64_v2(const double* a, double* partials_val, int64_t* partials_idx, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles_per_output, hipStream_t stream);
+
+/* ---- reduction final ---- */
+/* kernels.rs:289 */ void musapy_argmax_final_i64_v2(const int64_t* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:290 */ void musapy_argmax_final_f32_v2(const float* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:291 */ void musapy_argmax_final_f64_v2(const double* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:292 */ void musapy_argmin_final_i64_v2(const int64_t* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:293 */ void musapy_argmin_final_f32_v2(const float* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+/* kernels.rs:294 */ void musapy_argmin_final_f64_v2(const double* partials_val, const int64_t* partials_idx, int64_t* c, size_t num_partials, size_t out_size, hipStream_t stream);
+
+/* ---- arg reduction mid level ---- */
+/* kernels.rs:299 */ void musapy_argmax_mid_i64_v2(const int64_t* partials_val, const int64_t* partials_idx, int64_t* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+/* kernels.rs:300 */ void musapy_argmax_mid_f32_v2(const float* partials_val, const int64_t* partials_idx, float* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+/* kernels.rs:301 */ void musapy_argmax_mid_f64_v2(const double* partials_val, const int64_t* partials_idx, double* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+/* kernels.rs:302 */ void musapy_argmin_mid_i64_v2(const int64_t* partials_val, const int64_t* partials_idx, int64_t* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+/* kernels.rs:303 */ void musapy_argmin_mid_f32_v2(const float* partials_val, const int64_t* partials_idx, float* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+/* kernels.rs:304 */ void musapy_argmin_mid_f64_v2(const double* partials_val, const int64_t* partials_idx, double* out_val, int64_t* out_idx, size_t out_size, size_t tiles_per_output, size_t axis_len, hipStream_t stream);
+
+/* ---- view materialisation: stride-aware copy into a C-contiguous buffer ---- */
+/* kernels.rs:321 */ void musapy_copy_f32(const float* input, float* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+/* kernels.rs:322 */ void musapy_copy_f64(const double* input, double* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+/* kernels.rs:323 */ void musapy_copy_i32(const int32_t* input, int32_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+/* kernels.rs:324 */ void musapy_copy_i64(const int64_t* input, int64_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+/* new: 1- and 2-byte element copies (bool/int8/uint8, int16/uint16/float16/bfloat16 views) */
+void musapy_copy_u8(const uint8_t* input, uint8_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+void musapy_copy_u16(const uint16_t* input, uint16_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+
+/* ---- wrapper-level error (new; no counterpart in kernels.rs) ----
+ * Returns and clears the calling thread's last wrapper error: 0 none, 1 a cumsum scratch buffer
+ * that is NULL or smaller than the reference's scratch formula requires. */
+int musapy_kernels_take_error(void);
+
+/* ---- planning helper (new; no counterpart in kernels.rs) ----
+ * Tiles per output that the partial entry points should be given for this reduction on this
+ * device: 1 means a single-pass entry point already fills the GPU. */
+size_t musapy_reduce_tiles_hint(int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t elem_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MUSAPY_KERNELS_H */

@@ -1,0 +1,140 @@
+"""musapy_amd -- MI355X-native backend for musapy's stride-aware elementwise + reduction path.
+
+The Python surface mirrors musapy's (python/musapy/__init__.py re-exporting the PyO3 module):
+``ms.array``, ``ms.add`` ... ``ms.cumsum``, the same argument conventions, dtype strings
+('f32', 'i64', ...) and exception classes.  Arrays live on a HIP device ("hip:N"; "musa:N" is
+accepted as an alias so musapy code keeps working).  Every operator runs through the C-ABI
+kernel library ``libmusapy_hip.so``; importing fails loudly when it has not been built.
+"""
+from __future__ import annotations
+
+import os as _os
+
+import numpy as _np
+
+_here = _os.path.dirname(_os.path.abspath(__file__))
+try:
+    from . import _core
+except ImportError as _e:  # pragma: no cover - exercised only on an unbuilt tree
+    raise ImportError(
+        "musapy_amd native extension is not built (run `python -m musapy_amd.build`): " + str(_e)
+    ) from _e
+
+from ._core import (  # noqa: F401
+    Array, MusapyError, DeviceError, DeviceNotConfiguredError, DtypeError, ShapeError, MemoryError,
+    OutOfMemoryError, StreamError, KernelError,
+    add, sub, mul, div, pow, sin, cos, exp, log, abs, sign, neg, clamp, astype,
+    sum, prod, max, min, mean, argmax, argmin, cumsum,
+    transpose, flip, index_select, contiguous,
+    set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats,
+)
+
+__all__ = [
+    "Array", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp", "log",
+    "abs", "sign", "neg", "clamp", "astype", "sum", "prod", "max", "min", "mean", "argmax", "argmin",
+    "cumsum", "transpose", "permute", "flip", "slice", "index_select", "contiguous",
+]
+
+# dtype names (musapy exposes ms.float32 etc. as dtype objects; here they are the dtype strings)
+bool_ = "bool"
+int8, int16, int32, int64 = "i8", "i16", "i32", "i64"
+uint8, uint16, uint32, uint64 = "u8", "u16", "u32", "u64"
+float16, float32, float64, bfloat16 = "f16", "f32", "f64", "bf16"
+complex64, complex128 = "c64", "c128"
+
+_NP_OF = {"bool": _np.bool_, "i8": _np.int8, "i16": _np.int16, "i32": _np.int32, "i64": _np.int64,
+          "u8": _np.uint8, "u16": _np.uint16, "u32": _np.uint32, "u64": _np.uint64, "f16": _np.float16,
+          "f32": _np.float32, "f64": _np.float64, "c64": _np.complex64, "c128": _np.complex128}
+_ALIASES = {"float32": "f32", "float64": "f64", "float16": "f16", "bfloat16": "bf16", "int8": "i8",
+            "int16": "i16", "int32": "i32", "int64": "i64", "uint8": "u8", "uint16": "u16",
+            "uint32": "u32", "uint64": "u64", "complex64": "c64", "complex128": "c128", "bool_": "bool"}
+
+
+def _norm_dtype(d) -> str:
+    if d is None:
+        return None
+    if isinstance(d, _np.dtype) or (isinstance(d, type) and issubclass(d, _np.generic)):
+        d = _np.dtype(d).name
+    d = str(d)
+    return _ALIASES.get(d, d)
+
+
+def _contains_complex(x) -> bool:
+    if isinstance(x, complex):
+        return True
+    if isinstance(x, (list, tuple)):
+        return any(_contains_complex(v) for v in x)
+    return False
+
+
+def array(data, dtype=None, device=None) -> Array:
+    """``ms.array(data, dtype=None, device=None)`` (rust/musapy-python/src/ops.rs:28-101).
+
+    dtype resolution: explicit argument, else complex literals -> c128, else float32.
+    ``data`` may be a (nested) list/tuple, a scalar or a numpy array.
+    """
+    dt = _norm_dtype(dtype)
+    if dt is None:
+        if isinstance(data, _np.ndarray):
+            dt = "c128" if _np.iscomplexobj(data) else "f32"
+        else:
+            dt = "c128" if _contains_complex(data) else "f32"
+    if dt == "bf16":
+        host = _np.asarray(data)
+        if host.dtype != _np.uint16:
+            raise DtypeError("bf16 arrays are created from raw uint16 bit patterns")
+    else:
+        host = _np.asarray(data, dtype=_NP_OF[dt])
+    return _core._from_numpy(_np.ascontiguousarray(host), dt, device)
+
+
+def from_numpy(x, device=None) -> Array:
+    """Copy a numpy array (any dtype musapy knows) to the device, keeping its dtype."""
+    x = _np.ascontiguousarray(x)
+    name = {v: k for k, v in _ALIASES.items()}
+    dt = _ALIASES.get(x.dtype.name, x.dtype.name)
+    return _core._from_numpy(x, dt, device)
+
+
+def ones(shape, dtype="f32", device=None) -> Array:
+    dt = _norm_dtype(dtype)
+    if isinstance(shape, int):
+        shape = (shape,)
+    return array(_np.ones(shape, dtype=_NP_OF[dt]), dtype=dt, device=device)
+
+
+def permute(a: Array, axes) -> Array:
+    return transpose(a, list(axes))
+
+
+def slice(a: Array, ranges) -> Array:  # noqa: A001 - musapy name
+    """``ms.slice(a, [(start, stop, step), ...])`` (rust/musapy-core/src/layout.rs:214-259)."""
+    start = [r[0] for r in ranges]
+    stop = [r[1] for r in ranges]
+    step = [r[2] if len(r) > 2 else 1 for r in ranges]
+    return _core.slice(a, start, stop, step)
+
+
+def _tolist(self: Array):
+    if self.dtype in ("f16", "bf16"):
+        raise NotImplementedError(f"tolist() is not supported for {self.dtype} (as in musapy)")
+    return self.numpy().tolist()
+
+
+def _item(self: Array):
+    if self.size != 1:
+        raise ValueError(f"item() requires an array of size 1, got size {self.size}")
+    if self.dtype in ("f16", "bf16"):
+        raise NotImplementedError(f"item() is not supported for {self.dtype} (as in musapy)")
+    return self.numpy().reshape(-1)[0].item()
+
+
+def _repr(self: Array) -> str:
+    return f"Array(shape={self.shape}, dtype={self.dtype}, device={self.device})"
+
+
+Array.tolist = _tolist
+Array.item = _item
+Array.__repr__ = _repr
+Array.T = property(lambda self: transpose(self))
+Array.__len__ = lambda self: self.shape[0] if self.ndim else 0

@@ -1,0 +1,536 @@
+// elementwise.hip -- binary / unary / clamp / cast over N-d broadcast strides, for gfx950.
+//
+// Drop-in for the reference's kernels/elementwise.mu:577-828 (wrappers) and its nd / flat /
+// vec4 / scalar kernels (elementwise.mu:35-208, 295-394, 451-536).  Instead of one thread per
+// element decoding every dimension with 64-bit div/mod, the wrapper coalesces dimensions on the
+// host (plan.hpp) and picks one of four variants:
+//   flat       every operand contiguous or a broadcast scalar: 16-byte vector loads/stores,
+//              UNROLL independent vectors in flight per thread;
+//   rows       output rows of the innermost dim; the outer coordinates of a row are decoded
+//              once with 32-bit magic division, the inner dim is streamed per operand as
+//              vector (stride 1), broadcast (stride 0) or gather (any other stride);
+//   transpose  single-input ops whose input is unit-stride along some other dim (a transposed
+//              or permuted view): 64x64 tiles staged through LDS so both the read and the write
+//              are coalesced;
+//   generic    64-bit per-element decode, only for shapes beyond the 32-bit limits above.
+#include "kcommon.hpp"
+#include "ew_ops.hpp"
+#include "../../../include/musapy_kernels.h"
+
+namespace mpy {
+
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------------------------------------
+// operand access modes
+enum : int { kModeScalar = 0, kModeUnit = 1, kModeStrided = 2 };
+
+template <class T>
+struct In {
+  const T* p;
+  int mode;
+};
+
+// ---------------------------------------------------------------------------------------------
+// flat: 1-D, every input contiguous (mode 1) or scalar (mode 0).  Full tiles use VEC-wide
+// vector accesses; the final partial tile falls back to one element per lane.
+template <int VEC, int UNROLL, class F, class TO, class TA>
+__global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict__ c, uint64_t n, F f) {
+  constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
+  const uint64_t base = uint64_t(blockIdx.x) * kTile;
+  const int t = threadIdx.x;
+  if (base + kTile <= n) {
+    Vec<TA, VEC> va[UNROLL];
+    if (a.mode == kModeScalar) {
+      const TA s = a.p[0];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) va[u] = vload<TA, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      Vec<TO, VEC> vc;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k]);
+      vstore<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+    }
+  } else {
+    for (uint64_t i = base + t; i < n; i += kBlock) c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i]);
+  }
+}
+
+template <int VEC, int UNROLL, class F, class T>
+__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __restrict__ c, uint64_t n, F f) {
+  constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
+  const uint64_t base = uint64_t(blockIdx.x) * kTile;
+  const int t = threadIdx.x;
+  if (base + kTile <= n) {
+    Vec<T, VEC> va[UNROLL], vb[UNROLL];
+    if (a.mode == kModeScalar) {
+      const T s = a.p[0];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) va[u] = vload<T, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
+    }
+    if (b.mode == kModeScalar) {
+      const T s = b.p[0];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) vb[u].v[k] = s;
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) vb[u] = vload<T, VEC>(b.p + base + uint64_t(u * kBlock + t) * VEC);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      Vec<T, VEC> vc;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k], vb[u].v[k]);
+      vstore<T, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+    }
+  } else {
+    for (uint64_t i = base + t; i < n; i += kBlock)
+      c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i], b.mode == kModeScalar ? b.p[0] : b.p[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// rows: output rows of length L (the innermost coalesced dim).  A work item is VEC consecutive
+// elements of one row; `aligned` (host-checked) guarantees every item is full and every
+// unit-stride operand is 16-byte aligned at the item start.
+template <int VEC, class T>
+__device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t col, uint32_t L, bool full,
+                                 T (&x)[VEC]) {
+  if (mode == kModeScalar) {
+    const T v = base[0];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) x[k] = v;
+  } else if (mode == kModeUnit && full) {
+    Vec<T, VEC> v = vload<T, VEC>(base + col);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) x[k] = v.v[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k)
+      if (col + k < L) x[k] = base[int64_t(col + k) * s];
+  }
+}
+
+template <int VEC, int UNROLL, class F, class TO, class TA>
+__global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO* __restrict__ c, RowIndexer<2> ix,
+                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, F f) {
+  const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t g = first + u * kBlock;
+    if (g >= items) break;
+    const uint32_t row = fd_div(gpr, g);
+    const uint32_t col = (g - row * gpr.d) * VEC;
+    int64_t off[2];
+    row_offsets<2>(ix, row, off);
+    const bool full = aligned || (col + VEC <= L);
+    TA x[VEC];
+    load_item<VEC, TA>(a.p + off[1], a.mode, sa, col, L, full && aligned, x);
+    TO* cp = c + off[0] + col;
+    if (full && aligned) {
+      Vec<TO, VEC> v;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k]);
+      vstore<TO, VEC>(cp, v);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if (col + k < L) cp[k] = f(x[k]);
+    }
+  }
+}
+
+template <int VEC, int UNROLL, class F, class T>
+__global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<T> b, int64_t sb, T* __restrict__ c,
+                                                        RowIndexer<3> ix, FastDiv gpr, uint32_t L, uint32_t items,
+                                                        bool aligned, F f) {
+  const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t g = first + u * kBlock;
+    if (g >= items) break;
+    const uint32_t row = fd_div(gpr, g);
+    const uint32_t col = (g - row * gpr.d) * VEC;
+    int64_t off[3];
+    row_offsets<3>(ix, row, off);
+    const bool full = aligned || (col + VEC <= L);
+    T x[VEC], y[VEC];
+    load_item<VEC, T>(a.p + off[1], a.mode, sa, col, L, full && aligned, x);
+    load_item<VEC, T>(b.p + off[2], b.mode, sb, col, L, full && aligned, y);
+    T* cp = c + off[0] + col;
+    if (full && aligned) {
+      Vec<T, VEC> v;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k], y[k]);
+      vstore<T, VEC>(cp, v);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if (col + k < L) cp[k] = f(x[k], y[k]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// transpose: single input that is unit-stride along dim P while the output is unit-stride along
+// the innermost dim L.  A block moves a kTP x kTL tile through LDS.  Remaining dims are batch.
+constexpr int kTP = 64, kTL = 64;
+
+struct TransposeArgs {
+  uint64_t P, L;           // extents of the two tiled dims
+  int64_t in_sL;           // input stride along L (input stride along P is 1)
+  int64_t out_sP;          // output stride along P (output stride along L is 1)
+  FastDiv tilesL, tilesP;  // tile counts
+  RowIndexer<2> batch;     // batch dims: [0] output strides, [1] input strides
+};
+
+template <class F, class TO, class TI>
+__global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
+                                                            TransposeArgs ta, F f) {
+  __shared__ TO tile[kTL][kTP + 1];
+  uint32_t id = blockIdx.x;
+  const uint32_t bq = fd_div(ta.tilesL, id);
+  const uint32_t tl = id - bq * ta.tilesL.d;
+  const uint32_t batch = fd_div(ta.tilesP, bq);
+  const uint32_t tp = bq - batch * ta.tilesP.d;
+  int64_t off[2];
+  row_offsets<2>(ta.batch, batch, off);
+  const uint64_t p0 = uint64_t(tp) * kTP, l0 = uint64_t(tl) * kTL;
+  const TI* ab = a + off[1];
+  TO* cb = c + off[0];
+  const int t = threadIdx.x;
+  // read: lanes run along P (unit stride in the input)
+  {
+    const int pp = t % kTP;
+    for (int ll = t / kTP; ll < kTL; ll += kBlock / kTP) {
+      const uint64_t p = p0 + pp, l = l0 + ll;
+      if (p < ta.P && l < ta.L) tile[ll][pp] = f(ab[int64_t(l) * ta.in_sL + int64_t(p)]);
+    }
+  }
+  __syncthreads();
+  // write: lanes run along L (unit stride in the output)
+  {
+    const int ll = t % kTL;
+    for (int pp = t / kTL; pp < kTP; pp += kBlock / kTL) {
+      const uint64_t p = p0 + pp, l = l0 + ll;
+      if (p < ta.P && l < ta.L) cb[int64_t(p) * ta.out_sP + int64_t(l)] = tile[ll][pp];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// generic fallback: 64-bit decode per element (shapes beyond the 32-bit row limits).
+struct NdMeta64 {
+  int nd;
+  uint64_t shape[kMaxDims];
+  int64_t stride[3][kMaxDims];
+};
+
+__device__ inline void nd_offsets(const NdMeta64& m, uint64_t i, int nops, int64_t (&off)[3]) {
+  off[0] = off[1] = off[2] = 0;
+  for (int d = m.nd - 1; d >= 0; --d) {
+    uint64_t q = i / m.shape[d];
+    int64_t cd = int64_t(i - q * m.shape[d]);
+    i = q;
+    for (int o = 0; o < nops; ++o) off[o] += cd * m.stride[o][d];
+  }
+}
+
+template <class F, class TO, class TA>
+__global__ __launch_bounds__(kBlock) void k_unary_generic(const TA* __restrict__ a, TO* __restrict__ c, NdMeta64 m,
+                                                          uint64_t n, F f) {
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += uint64_t(gridDim.x) * kBlock) {
+    int64_t off[3];
+    nd_offsets(m, i, 2, off);
+    c[off[0]] = f(a[off[1]]);
+  }
+}
+
+template <class F, class T>
+__global__ __launch_bounds__(kBlock) void k_binary_generic(const T* __restrict__ a, const T* __restrict__ b,
+                                                           T* __restrict__ c, NdMeta64 m, uint64_t n, F f) {
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += uint64_t(gridDim.x) * kBlock) {
+    int64_t off[3];
+    nd_offsets(m, i, 3, off);
+    c[off[0]] = f(a[off[1]], b[off[2]]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// host side: variant selection
+constexpr int kUnroll = 4;
+
+template <class T>
+constexpr int vec_of() {
+  return sizeof(T) >= 8 ? 2 : (sizeof(T) == 4 ? 4 : 8);
+}
+template <class TA, class TO>
+constexpr int ew_vec() {
+  constexpr size_t m = sizeof(TA) < sizeof(TO) ? sizeof(TA) : sizeof(TO);
+  return m >= 8 ? 2 : (m == 4 ? 4 : 8);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int mode_of(int64_t s) { return s == 0 ? kModeScalar : (s == 1 ? kModeUnit : kModeStrided); }
+
+inline NdMeta64 make_meta64(const Plan& p) {
+  NdMeta64 m{};
+  m.nd = p.ndim;
+  for (int d = 0; d < p.ndim; ++d) {
+    m.shape[d] = p.shape[d];
+    for (int o = 0; o < p.nops && o < 3; ++o) m.stride[o][d] = p.stride[o][d];
+  }
+  return m;
+}
+
+inline unsigned grid_generic(uint64_t n) {
+  uint64_t g = (n + kBlock - 1) / kBlock;
+  return unsigned(g > 65536 ? 65536 : g);
+}
+
+// rows path limits: row count and items must fit 32 bits
+inline bool rows_ok(const Plan& p, int vec) {
+  uint64_t L = p.shape[p.ndim - 1];
+  uint64_t rows = p.numel / L;
+  uint64_t items = rows * ((L + vec - 1) / vec);
+  if (L >= (uint64_t(1) << 31) || items >= (uint64_t(1) << 31)) return false;
+  for (int d = 0; d < p.ndim - 1; ++d)
+    if (p.shape[d] >= (uint64_t(1) << 32)) return false;
+  return true;
+}
+
+// true when every unit-stride operand starts 16-byte aligned at each VEC item of every row
+template <class T0, class T1, class T2 = T1>
+inline bool rows_aligned(const Plan& p, int vec, const void* c, const void* a, const void* b = nullptr) {
+  uint64_t L = p.shape[p.ndim - 1];
+  if (L % vec) return false;
+  const void* ptr[3] = {c, a, b};
+  const size_t es[3] = {sizeof(T0), sizeof(T1), sizeof(T2)};
+  for (int o = 0; o < p.nops; ++o) {
+    int64_t s = p.stride[o][p.ndim - 1];
+    if (s != 1) continue;
+    if (es[o] * vec < 16 ? (reinterpret_cast<uintptr_t>(ptr[o]) % (es[o] * vec)) : !aligned16(ptr[o])) return false;
+    for (int d = 0; d < p.ndim - 1; ++d) {
+      uint64_t bytes = uint64_t(p.stride[o][d] < 0 ? -p.stride[o][d] : p.stride[o][d]) * es[o];
+      if (bytes % (es[o] * vec < 16 ? es[o] * vec : 16)) return false;
+    }
+  }
+  return true;
+}
+
+template <class F, class TO, class TA>
+void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize_t* as, hipStream_t st, F f) {
+  Plan p;
+  const ssize_t* ins[1] = {as};
+  if (!plan_elementwise(p, ndim, shape, 1, ins)) return;
+  // the narrower type moves 16 bytes per item, the wider one 16-32 (e.g. f64->f32: 4 elements)
+  constexpr int V = ew_vec<TA, TO>();
+  if (p.ndim == 1 && p.stride[0][0] == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1)) {
+    In<TA> ia{a, mode_of(p.stride[1][0])};
+    bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a));
+    if (vec_ok) {
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kUnroll - 1) / (uint64_t(kBlock) * V * kUnroll);
+      k_unary_flat<V, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
+    } else {
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
+      k_unary_flat<1, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
+    }
+    return;
+  }
+  // transposed input: unit stride along some dim other than the innermost one
+  const int nd = p.ndim;
+  const int64_t sL = p.stride[1][nd - 1];
+  if (nd >= 2 && sL != 0 && sL != 1) {
+    int P = -1;
+    for (int d = nd - 2; d >= 0; --d)
+      if (p.stride[1][d] == 1) { P = d; break; }
+    if (P >= 0 && p.shape[P] < (uint64_t(1) << 32) && p.shape[nd - 1] < (uint64_t(1) << 32)) {
+      TransposeArgs ta{};
+      ta.P = p.shape[P];
+      ta.L = p.shape[nd - 1];
+      ta.in_sL = sL;
+      ta.out_sP = p.stride[0][P];
+      uint64_t tL = (ta.L + kTL - 1) / kTL, tP = (ta.P + kTP - 1) / kTP;
+      uint64_t nb = p.numel / (ta.P * ta.L);
+      if (tL * tP * nb < (uint64_t(1) << 31)) {
+        ta.tilesL = make_fastdiv(uint32_t(tL));
+        ta.tilesP = make_fastdiv(uint32_t(tP));
+        // batch dims: all dims but P and nd-1, innermost first
+        ta.batch.nd = 0;
+        for (int d = nd - 2; d >= 0; --d) {
+          if (d == P) continue;
+          int k = ta.batch.nd++;
+          ta.batch.div[k] = make_fastdiv(uint32_t(p.shape[d]));
+          ta.batch.stride[0][k] = p.stride[0][d];
+          ta.batch.stride[1][k] = p.stride[1][d];
+        }
+        k_unary_transpose<F, TO, TA><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
+        return;
+      }
+    }
+  }
+  if (nd >= 2 && rows_ok(p, V)) {
+    const uint32_t L = uint32_t(p.shape[nd - 1]);
+    In<TA> ia{a, mode_of(sL)};
+    bool al = rows_aligned<TO, TA>(p, V, c, a);
+    uint32_t gpr = (L + V - 1) / V;
+    uint32_t items = uint32_t(p.numel / L) * gpr;
+    RowIndexer<2> ix = make_row_indexer<2>(p);
+    unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+    k_unary_rows<V, kUnroll, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items, al, f);
+    return;
+  }
+  k_unary_generic<F, TO, TA><<<grid_generic(p.numel), kBlock, 0, st>>>(a, c, make_meta64(p), p.numel, f);
+}
+
+template <class F, class T>
+void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, const ssize_t* as, const ssize_t* bs,
+                   hipStream_t st, F f) {
+  Plan p;
+  const ssize_t* ins[2] = {as, bs};
+  if (!plan_elementwise(p, ndim, shape, 2, ins)) return;
+  constexpr int V = vec_of<T>();
+  const int nd = p.ndim;
+  if (nd == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1) && (p.stride[2][0] == 0 || p.stride[2][0] == 1)) {
+    In<T> ia{a, mode_of(p.stride[1][0])}, ib{b, mode_of(p.stride[2][0])};
+    bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a)) && (ib.mode == kModeScalar || aligned16(b));
+    if (vec_ok) {
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kUnroll - 1) / (uint64_t(kBlock) * V * kUnroll);
+      k_binary_flat<V, kUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+    } else {
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
+      k_binary_flat<1, kUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+    }
+    return;
+  }
+  if (rows_ok(p, V)) {
+    const uint32_t L = uint32_t(p.shape[nd - 1]);
+    const int64_t sa = p.stride[1][nd - 1], sb = p.stride[2][nd - 1];
+    In<T> ia{a, mode_of(sa)}, ib{b, mode_of(sb)};
+    bool al = rows_aligned<T, T, T>(p, V, c, a, b);
+    uint32_t gpr = (L + V - 1) / V;
+    uint32_t items = uint32_t(p.numel / L) * gpr;
+    RowIndexer<3> ix = make_row_indexer<3>(p);
+    unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+    k_binary_rows<V, kUnroll, F, T><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al, f);
+    return;
+  }
+  k_binary_generic<F, T><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
+}
+
+}  // namespace mpy
+
+// =============================================================================================
+// extern "C" surface (rust/musapy-ops/src/kernels.rs:19-81; new bf16/f16 casts)
+using namespace mpy;
+
+extern "C" {
+
+#define MPY_BINARY(NAME, F)                                                                                 \
+  void musapy_##NAME##_f32_v2(const float* a, const float* b, float* c, int ndim, const size_t* shape,      \
+                              const ssize_t* as, const ssize_t* bs, hipStream_t st) {                      \
+    launch_binary<F, float>(a, b, c, ndim, shape, as, bs, st, F{});                                        \
+  }                                                                                                         \
+  void musapy_##NAME##_f64_v2(const double* a, const double* b, double* c, int ndim, const size_t* shape,   \
+                              const ssize_t* as, const ssize_t* bs, hipStream_t st) {                      \
+    launch_binary<F, double>(a, b, c, ndim, shape, as, bs, st, F{});                                       \
+  }
+MPY_BINARY(add, AddF)
+MPY_BINARY(sub, SubF)
+MPY_BINARY(mul, MulF)
+MPY_BINARY(div, DivF)
+MPY_BINARY(pow, PowF)
+#undef MPY_BINARY
+
+#define MPY_UNARY(NAME, F)                                                                                  \
+  void musapy_##NAME##_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* as,   \
+                              hipStream_t st) {                                                             \
+    launch_unary<F, float, float>(a, c, ndim, shape, as, st, F{});                                         \
+  }                                                                                                         \
+  void musapy_##NAME##_f64_v2(const double* a, double* c, int ndim, const size_t* shape, const ssize_t* as, \
+                              hipStream_t st) {                                                             \
+    launch_unary<F, double, double>(a, c, ndim, shape, as, st, F{});                                       \
+  }
+MPY_UNARY(sin, SinF)
+MPY_UNARY(cos, CosF)
+MPY_UNARY(exp, ExpF)
+MPY_UNARY(log, LogF)
+MPY_UNARY(abs, AbsF)
+MPY_UNARY(sign, SignF)
+MPY_UNARY(neg, NegF)
+#undef MPY_UNARY
+
+void musapy_clamp_f32_v2(const float* a, float* c, float lo, float hi, int ndim, const size_t* shape,
+                         const ssize_t* as, hipStream_t st) {
+  launch_unary<ClampF<float>, float, float>(a, c, ndim, shape, as, st, ClampF<float>{lo, hi});
+}
+void musapy_clamp_f64_v2(const double* a, double* c, double lo, double hi, int ndim, const size_t* shape,
+                         const ssize_t* as, hipStream_t st) {
+  launch_unary<ClampF<double>, double, double>(a, c, ndim, shape, as, st, ClampF<double>{lo, hi});
+}
+
+#define MPY_CAST(SN, ST, DN, DT)                                                                            \
+  void musapy_cast_##SN##_##DN##_v2(const ST* a, DT* c, int ndim, const size_t* shape, const ssize_t* as,   \
+                                     hipStream_t st) {                                                      \
+    launch_unary<CastF<ST, DT>, DT, ST>(a, c, ndim, shape, as, st, CastF<ST, DT>{});                       \
+  }
+#define MPY_CAST_FROM_INTS(DN, DT)    \
+  MPY_CAST(i8, int8_t, DN, DT)        \
+  MPY_CAST(i16, int16_t, DN, DT)      \
+  MPY_CAST(i32, int32_t, DN, DT)      \
+  MPY_CAST(u8, uint8_t, DN, DT)       \
+  MPY_CAST(u16, uint16_t, DN, DT)     \
+  MPY_CAST(u32, uint32_t, DN, DT)     \
+  MPY_CAST(u64, uint64_t, DN, DT)
+MPY_CAST_FROM_INTS(f32, float)
+MPY_CAST(i64, int64_t, f32, float)
+MPY_CAST(f64, double, f32, float)
+MPY_CAST_FROM_INTS(f64, double)
+MPY_CAST(i64, int64_t, f64, double)
+MPY_CAST(f32, float, f64, double)
+MPY_CAST_FROM_INTS(i64, int64_t)
+MPY_CAST(f32, float, i64, int64_t)
+MPY_CAST(f64, double, i64, int64_t)
+#undef MPY_CAST_FROM_INTS
+#undef MPY_CAST
+
+void musapy_cast_f32_bf16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* as,
+                             hipStream_t st) {
+  launch_unary<ToBf16F, uint16_t, float>(a, c, ndim, shape, as, st, ToBf16F{});
+}
+void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* as,
+                            hipStream_t st) {
+  launch_unary<ToF16F, uint16_t, float>(a, c, ndim, shape, as, st, ToF16F{});
+}
+
+// stride-aware materialisation of a view (kernels.rs:321-324; u8/u16 are new, for 1- and
+// 2-byte dtypes).  A transposed source takes the LDS-tiled path.
+#define MPY_COPY(NAME, T)                                                                                    \
+  void musapy_copy_##NAME(const T* input, T* output, int ndim, const size_t* shape, const ssize_t* in_strides, \
+                          hipStream_t st) {                                                                   \
+    launch_unary<IdentityF, T, T>(input, output, ndim, shape, in_strides, st, IdentityF{});                  \
+  }
+MPY_COPY(f32, float)
+MPY_COPY(f64, double)
+MPY_COPY(i32, int32_t)
+MPY_COPY(i64, int64_t)
+MPY_COPY(u8, uint8_t)
+MPY_COPY(u16, uint16_t)
+#undef MPY_COPY
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// kcommon.hpp -- device/host helpers shared by the gfx950 kernels.
+//
+// Replaces kernels/include/common.h of the reference (offset_nd / reduce_input_offset,
+// common.h:42-79), which recomputes a 64-bit div/mod per dimension, per operand, per element.
+// Here the host coalesces dimensions first and the device divides with precomputed 32-bit
+// magic numbers, once per row rather than once per element.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <sys/types.h>
+
+#include "plan.hpp"
+#include "../../../include/musapy_kernels.h"
+
+namespace mpy {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---------------------------------------------------------------------------------------------
+// device side of the magic-number division of plan.hpp (FastDiv)
+__device__ inline uint32_t fd_div(const FastDiv& f, uint32_t n) {
+  uint32_t t = __umulhi(n, f.m);
+  return uint32_t((uint64_t(t) + n) >> f.s);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Offsets of the outer (non-innermost) coordinates of a row, for up to NOPS operands.
+// Dims are stored innermost-first; dim sizes < 2^32, row index < 2^32 (host checks).
+template <int NOPS>
+struct RowIndexer {
+  int nd;                       // number of outer dims
+  FastDiv div[kMaxDims];
+  int64_t stride[NOPS][kMaxDims];
+};
+
+template <int NOPS>
+__device__ inline void row_offsets(const RowIndexer<NOPS>& ix, uint32_t row, int64_t (&off)[NOPS]) {
+#pragma unroll
+  for (int o = 0; o < NOPS; ++o) off[o] = 0;
+  for (int i = 0; i < ix.nd; ++i) {
+    uint32_t q = fd_div(ix.div[i], row);
+    uint32_t c = row - q * ix.div[i].d;
+    row = q;
+#pragma unroll
+    for (int o = 0; o < NOPS; ++o) off[o] += int64_t(c) * ix.stride[o][i];
+  }
+}
+
+template <int NOPS>
+inline RowIndexer<NOPS> make_row_indexer(const Plan& p) {
+  RowIndexer<NOPS> ix{};
+  ix.nd = p.ndim - 1;
+  for (int i = 0; i < ix.nd; ++i) {
+    int dim = p.ndim - 2 - i;  // innermost outer dim first
+    ix.div[i] = make_fastdiv(uint32_t(p.shape[dim]));
+    for (int o = 0; o < NOPS; ++o) ix.stride[o][i] = p.stride[o][dim];
+  }
+  return ix;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Aligned vector of N elements: one global_load_dwordx4 per 16 bytes.
+template <typename T, int N>
+struct alignas(sizeof(T) * N >= 16 ? 16 : sizeof(T) * N) Vec {
+  T v[N];
+};
+
+template <typename T, int N>
+__device__ inline Vec<T, N> vload(const T* p) {
+  return *reinterpret_cast<const Vec<T, N>*>(p);
+}
+template <typename T, int N>
+__device__ inline void vstore(T* p, const Vec<T, N>& v) {
+  *reinterpret_cast<Vec<T, N>*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wavefront-64 butterfly helpers (ds_swizzle/dpp are chosen by the compiler for __shfl_xor).
+template <typename T>
+__device__ inline T shfl_xor(T v, int m) {
+  return __shfl_xor(v, m, kWave);
+}
+
+// interleaved complex elements, the ABI types themselves
+using c64 = musapy_c64_t;
+using c128 = musapy_c128_t;
+
+}  // namespace mpy

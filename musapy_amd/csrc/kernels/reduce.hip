@@ -1,0 +1,522 @@
+// reduce.hip -- sum / prod / max / min / mean / argmax / argmin over one axis, for gfx950.
+//
+// Drop-in for the reference's kernels/reduction.mu:1342-2055 (the `_v2` wrappers: naive,
+// small_axis, partial, final, mid).  All entry points share two streaming kernels chosen from
+// the host plan (plan.hpp):
+//   row  the reduced axis is the walk direction: a group of lanes (a whole block, one wave, or a
+//        single lane for very short axes) reduces one (output, tile) segment with 16-byte loads
+//        when the axis is unit-stride, then combines through wave-64 butterflies and LDS;
+//   col  the reduced axis is strided but the innermost output dim is unit-stride (axis=0 of a
+//        C-order matrix): 64 lanes x VEC walk adjacent columns, the 4 waves of a block split the
+//        rows, and LDS merges the waves -- every load is a coalesced row segment.
+// Large reductions are split into tiles: the partial entry points write [out_size][tiles] and
+// the final entry points reduce those rows with the same row kernel.  Every combine order is
+// fixed, so results are identical from run to run.
+#include "kcommon.hpp"
+#include "reduce_ops.hpp"
+#include "../../../include/musapy_kernels.h"
+
+namespace mpy {
+
+constexpr int kRBlock = 256;
+
+// what a kernel writes per (output, tile)
+enum : int { kWriteFinal = 0, kWriteVal = 1, kWritePair = 2 };
+// which final transform applies to an additive accumulator
+enum : int { kFinPlain = 0, kFinMean = 1 };
+
+template <class T>
+struct RedOut {
+  T* val;            // final values (kWriteFinal of value ops) or partial values
+  int64_t* idx;      // arg results (kWriteFinal of arg ops) or partial indices
+  double count;      // mean divisor
+  int fin;
+};
+
+// --------------------------------------------------------------------------------------------
+// Writing one finished accumulator.
+template <class Op, class T, int WRITE>
+__device__ inline void write_result(const RedOut<T>& out, uint64_t slot, typename Op::A acc) {
+  if constexpr (Op::kOrdered) {
+    if constexpr (WRITE == kWritePair) {
+      out.val[slot] = acc.idx < 0 ? T(0) : acc.val;
+      out.idx[slot] = acc.idx;
+    } else if constexpr (Op::kArg) {  // final arg result
+      out.idx[slot] = acc.idx < 0 ? 0 : acc.idx;
+    } else {
+      // value max/min: an empty tile writes a marker the next level skips
+      if (acc.idx < 0)
+        out.val[slot] = Op::better(T(1), T(0)) ? ext_none<T>() : ext_none_min<T>();
+      else
+        out.val[slot] = acc.val;
+    }
+  } else {
+    if (WRITE == kWriteFinal && out.fin == kFinMean)
+      out.val[slot] = mean_of<T>(acc, out.count);
+    else
+      out.val[slot] = narrow<T>(acc);
+  }
+}
+
+// NaN at axis position 0 absorbs the whole max/min/arg scan (see reduce_ops.hpp).
+template <class Op, class T>
+__device__ inline typename Op::A absorb_first(typename Op::A acc, T first) {
+  if constexpr (Op::kOrdered) {
+    if (is_nan(first)) {
+      acc.val = first;
+      acc.idx = 0;
+    }
+  }
+  return acc;
+}
+
+// --------------------------------------------------------------------------------------------
+// Group reduction (GROUP lanes -> lane 0 of the group holds the result).
+template <class Op, int GROUP>
+__device__ inline typename Op::A group_reduce(typename Op::A acc) {
+  using A = typename Op::A;
+  if constexpr (GROUP > 1) {
+    constexpr int W = GROUP < kWave ? GROUP : kWave;
+#pragma unroll
+    for (int m = W / 2; m >= 1; m >>= 1) acc = Op::comb(acc, acc_shfl(acc, m));
+  }
+  if constexpr (GROUP > kWave) {
+    __shared__ A part[GROUP / kWave];
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    if (lane == 0) part[w] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 1; i < GROUP / kWave; ++i) acc = Op::comb(acc, part[i]);
+    }
+  }
+  return acc;
+}
+
+// --------------------------------------------------------------------------------------------
+// row kernel: work item w = o * tiles + t, o = output index, t = tile along the axis
+struct RowArgs {
+  RowIndexer<1> ix;   // output coordinates -> input offset
+  uint64_t R;         // axis length
+  int64_t rs;         // axis stride
+  uint64_t chunk;     // axis elements per tile (multiple of VEC when VEC > 1)
+  uint32_t tiles;
+  uint64_t nwork;     // out_size * tiles
+};
+
+template <class Op, class T, int GROUP, int VEC, int UNROLL, int WRITE>
+__global__ __launch_bounds__(kRBlock) void k_reduce_row(const T* __restrict__ a, RowArgs ra, RedOut<T> out) {
+  using A = typename Op::A;
+  constexpr int kPer = kRBlock / GROUP;  // items per block
+  const uint64_t w = uint64_t(blockIdx.x) * kPer + threadIdx.x / GROUP;
+  const int l = threadIdx.x % GROUP;
+  const bool live = w < ra.nwork;
+  A acc = Op::init();
+  uint64_t o = 0, t = 0;
+  const T* base = a;
+  if (live) {
+    o = w / ra.tiles;
+    t = w - o * ra.tiles;
+    int64_t off[1];
+    row_offsets<1>(ra.ix, uint32_t(o), off);
+    base = a + off[0];
+    uint64_t k0 = t * ra.chunk;
+    uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
+    uint64_t k = k0 + uint64_t(l) * VEC;
+    constexpr uint64_t stepk = uint64_t(GROUP) * VEC;
+    if (VEC > 1) {
+      for (; k + (UNROLL - 1) * stepk + VEC <= k1; k += UNROLL * stepk) {
+        Vec<T, VEC> x[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(base + k + u * stepk);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x[u].v[v], int64_t(k + u * stepk + v));
+      }
+      for (; k < k1; k += stepk)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (k + v < k1) acc = Op::step(acc, base[k + v], int64_t(k + v));
+    } else {
+      const int64_t rs = ra.rs;
+      for (; k + (UNROLL - 1) * stepk < k1; k += UNROLL * stepk) {
+        T x[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) x[u] = base[int64_t(k + u * stepk) * rs];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
+      }
+      for (; k < k1; k += stepk) acc = Op::step(acc, base[int64_t(k) * rs], int64_t(k));
+    }
+  }
+  acc = group_reduce<Op, GROUP>(acc);
+  if (live && (GROUP <= kWave ? l == 0 : threadIdx.x == 0)) {
+    if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
+    write_result<Op, T, WRITE>(out, w, acc);
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// col kernel: block = (outer, column group, tile); 64 lanes x VEC columns, 4 waves split rows.
+struct ColArgs {
+  RowIndexer<1> ix;   // outer output dims (all but the innermost one) -> input offset
+  uint64_t C;         // innermost output extent (unit stride in the input)
+  uint32_t cgroups;   // ceil(C / (64 * VEC))
+  uint64_t R;
+  int64_t rs;
+  uint64_t chunk;
+  uint32_t tiles;
+};
+
+template <class Op, class T, int VEC, int UNROLL, int WRITE>
+__global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
+                                                        bool vec_ok) {
+  using A = typename Op::A;
+  constexpr int kWaves = kRBlock / kWave;
+  __shared__ A part[kWaves - 1][kWave * VEC];
+  const uint32_t b = blockIdx.x;
+  const uint32_t t = b % ca.tiles;
+  const uint32_t rest = b / ca.tiles;
+  const uint32_t cg = rest % ca.cgroups;
+  const uint32_t outer = rest / ca.cgroups;
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  int64_t off[1];
+  row_offsets<1>(ca.ix, outer, off);
+  const uint64_t c0 = uint64_t(cg) * kWave * VEC + uint64_t(lane) * VEC;
+  const T* base = a + off[0] + c0;
+  const bool full = vec_ok && c0 + VEC <= ca.C;
+  const uint64_t k0 = uint64_t(t) * ca.chunk;
+  const uint64_t k1 = k0 + ca.chunk < ca.R ? k0 + ca.chunk : ca.R;
+  A acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = Op::init();
+  if (c0 < ca.C) {
+    uint64_t k = k0 + wv;
+    if (full) {
+      for (; k + (UNROLL - 1) * kWaves < k1; k += UNROLL * kWaves) {
+        Vec<T, VEC> x[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x[u].v[v], int64_t(k + u * kWaves));
+      }
+      for (; k < k1; k += kWaves) {
+        Vec<T, VEC> x = vload<T, VEC>(base + int64_t(k) * ca.rs);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k));
+      }
+    } else {
+      for (; k < k1; k += kWaves)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (c0 + v < ca.C) acc[v] = Op::step(acc[v], base[int64_t(k) * ca.rs + v], int64_t(k));
+    }
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) part[wv - 1][lane * VEC + v] = acc[v];
+  }
+  __syncthreads();
+  if (wv == 0 && c0 < ca.C) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      if (c0 + v >= ca.C) break;
+      A r = acc[v];
+#pragma unroll
+      for (int i = 0; i < kWaves - 1; ++i) r = Op::comb(r, part[i][lane * VEC + v]);
+      if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, base[v]);
+      const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
+      write_result<Op, T, WRITE>(out, o * ca.tiles + t, r);
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// pair kernel (arg final / mid): rows of (value, index) partials, contiguous [out][n]
+template <class Op, class T, int WRITE>
+__global__ __launch_bounds__(kRBlock) void k_reduce_pairs(const T* __restrict__ pv, const int64_t* __restrict__ pi,
+                                                          uint64_t n, uint64_t chunk, uint32_t tiles, uint64_t nwork,
+                                                          RedOut<T> out) {
+  using A = typename Op::A;
+  const uint64_t w = uint64_t(blockIdx.x) * (kRBlock / kWave) + threadIdx.x / kWave;
+  const int l = threadIdx.x % kWave;
+  A acc = Op::init();
+  uint64_t o = 0, t = 0;
+  if (w < nwork) {
+    o = w / tiles;
+    t = w - o * tiles;
+    uint64_t k0 = t * chunk, k1 = k0 + chunk < n ? k0 + chunk : n;
+    for (uint64_t k = k0 + l; k < k1; k += kWave) acc = Op::step_pair(acc, pv[o * n + k], pi[o * n + k]);
+  }
+  acc = group_reduce<Op, kWave>(acc);
+  if (w < nwork && l == 0) {
+    if (t == 0 && is_nan(pv[o * n]) && pi[o * n] >= 0) {  // the level below was absorbed by x[0]
+      acc.val = pv[o * n];
+      acc.idx = pi[o * n];
+    }
+    write_result<Op, T, WRITE>(out, w, acc);
+  }
+}
+
+// ============================================================================================
+// host side
+inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+template <class T> constexpr int rvec() { return sizeof(T) >= 16 ? 1 : int(16 / sizeof(T)); }
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline RowIndexer<1> out_indexer(const ReducePlan& p, int ndims) {
+  // first `ndims` output dims (outermost first) as a row indexer, innermost first
+  RowIndexer<1> ix{};
+  ix.nd = ndims;
+  for (int i = 0; i < ndims; ++i) {
+    int d = ndims - 1 - i;
+    ix.div[i] = make_fastdiv(uint32_t(p.oshape[d]));
+    ix.stride[0][i] = p.ostride[d];
+  }
+  return ix;
+}
+
+// Recommended tiles per output: enough (output, tile) work items to fill 256 CUs several times
+// over while each tile still streams a few tens of KB.
+inline size_t tiles_hint(const ReducePlan& p, size_t es) {
+  if (p.R <= 1 || p.out_size == 0) return 1;
+  const uint64_t want_items = 2048;
+  if (p.kind == kColReduce) {
+    const int vec = int(16 / es) > 0 ? int(16 / es) : 1;
+    uint64_t C = p.oshape[p.ond - 1];
+    uint64_t blocks = (p.out_size / C) * ceil_div(C, uint64_t(kWave) * vec);
+    if (blocks >= want_items) return 1;
+    uint64_t tiles = ceil_div(want_items, blocks);
+    uint64_t max_tiles = ceil_div(p.R, 64);  // keep >= 64 rows per tile
+    if (tiles > max_tiles) tiles = max_tiles;
+    return size_t(tiles < 1 ? 1 : tiles);
+  }
+  if (p.out_size >= want_items) return 1;
+  uint64_t tiles = ceil_div(want_items, p.out_size);
+  uint64_t max_tiles = ceil_div(p.R * es, 32768);  // >= 32 KB per tile
+  if (tiles > max_tiles) tiles = max_tiles;
+  return size_t(tiles < 1 ? 1 : tiles);
+}
+
+template <class Op, class T, int WRITE>
+void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                   size_t axis_len, size_t out_size, size_t tiles, hipStream_t st) {
+  if (out_size == 0) return;  // axis_len == 0 still writes the identity (0 for sums, 1 for products)
+  if (tiles < 1) tiles = 1;
+  ReducePlan p;
+  plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
+  // `tiles` is the caller's partial layout: every slot is written, tiles past the end of the
+  // axis hold the operation's "empty" value
+  constexpr int V = rvec<T>();
+  if (p.kind == kColReduce && p.oshape[p.ond - 1] < (uint64_t(1) << 31)) {
+    ColArgs ca{};
+    ca.ix = out_indexer(p, p.ond - 1);
+    ca.C = p.oshape[p.ond - 1];
+    ca.cgroups = uint32_t(ceil_div(ca.C, uint64_t(kWave) * V));
+    ca.R = p.R;
+    ca.rs = p.rstride;
+    ca.chunk = ceil_div(p.R, tiles);
+    ca.tiles = uint32_t(tiles);
+    bool vec_ok = al16(a) && (ca.C % V == 0) && ((uint64_t(p.rstride < 0 ? -p.rstride : p.rstride) * sizeof(T)) % 16 == 0);
+    for (int d = 0; d < p.ond - 1; ++d)
+      if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) vec_ok = false;
+    const uint64_t blocks = (p.out_size / ca.C) * ca.cgroups * ca.tiles;
+    k_reduce_col<Op, T, V, 4, WRITE><<<dim3(unsigned(blocks)), kRBlock, 0, st>>>(a, ca, out, vec_ok);
+    return;
+  }
+  RowArgs ra{};
+  ra.ix = out_indexer(p, p.ond);
+  ra.R = p.R;
+  ra.rs = p.rstride;
+  ra.tiles = uint32_t(tiles);
+  uint64_t chunk = ceil_div(p.R, tiles);
+  bool vec_ok = (p.rstride == 1) && al16(a);
+  for (int d = 0; d < p.ond; ++d)
+    if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) vec_ok = false;
+  if (vec_ok && V > 1) chunk = ceil_div(chunk, V) * V;
+  ra.chunk = chunk;
+  ra.nwork = uint64_t(out_size) * tiles;
+  const uint64_t seg = chunk;
+  if (seg >= 4096) {
+    unsigned grid = unsigned(ra.nwork);
+    if (vec_ok)
+      k_reduce_row<Op, T, kRBlock, V, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+    else
+      k_reduce_row<Op, T, kRBlock, 1, 8, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+  } else if (seg >= 64) {
+    unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock / kWave));
+    if (vec_ok)
+      k_reduce_row<Op, T, kWave, V, 2, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+    else
+      k_reduce_row<Op, T, kWave, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+  } else {
+    unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock));
+    k_reduce_row<Op, T, 1, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+  }
+}
+
+// final over [out_size][num_partials] contiguous partials: the row kernel with unit stride
+template <class Op, class T>
+void launch_final(const T* partials, RedOut<T> out, size_t num_partials, size_t out_size, hipStream_t st) {
+  size_t shape[2] = {out_size, num_partials};
+  ssize_t strides[2] = {ssize_t(num_partials), 1};
+  launch_reduce<Op, T, kWriteFinal>(partials, out, 2, shape, strides, 1, num_partials, out_size, 1, st);
+}
+
+template <class Op, class T, int WRITE>
+void launch_pairs(const T* pv, const int64_t* pi, RedOut<T> out, size_t n, size_t out_size, size_t tiles,
+                  hipStream_t st) {
+  if (out_size == 0 || n == 0) return;
+  if (tiles < 1) tiles = 1;
+  uint64_t chunk = ceil_div(n, tiles);
+  uint64_t nwork = uint64_t(out_size) * tiles;
+  unsigned grid = unsigned(ceil_div(nwork, kRBlock / kWave));
+  k_reduce_pairs<Op, T, WRITE><<<grid, kRBlock, 0, st>>>(pv, pi, n, chunk, uint32_t(tiles), nwork, out);
+}
+
+// count produced by "+1" repeated axis_len times in T (cpu_mean_typed, op_builder.rs:3608-3612)
+template <class T> inline double mean_count(size_t n) {
+  if (sizeof(T) == 4) return double(n > (size_t(1) << 24) ? (size_t(1) << 24) : n);
+  return double(n > (size_t(1) << 53) ? (size_t(1) << 53) : n);
+}
+
+template <class T> inline RedOut<T> vout(T* c) { return RedOut<T>{c, nullptr, 0.0, kFinPlain}; }
+template <class T> inline RedOut<T> iout(int64_t* c) { return RedOut<T>{nullptr, c, 0.0, kFinPlain}; }
+template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c, nullptr, cnt, kFinMean}; }
+
+}  // namespace mpy
+
+
+// =============================================================================================
+// extern "C" surface (rust/musapy-ops/src/kernels.rs:139-183, 222-305)
+using namespace mpy;
+
+namespace mpy {
+template <class T> using OpMax = OpExt<T, true, false>;
+template <class T> using OpMin = OpExt<T, false, false>;
+template <class T> using OpArgmax = OpExt<T, true, true>;
+template <class T> using OpArgmin = OpExt<T, false, true>;
+}  // namespace mpy
+
+#define RED_ARGS int ndim, const size_t *in_shape, const ssize_t *in_strides, int axis, size_t axis_len, size_t out_size
+#define RED_PASS ndim, in_shape, in_strides, axis, axis_len, out_size
+
+extern "C" {
+
+size_t musapy_reduce_tiles_hint(int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis,
+                                size_t axis_len, size_t out_size, size_t elem_size) {
+  if (out_size == 0 || axis_len == 0) return 1;
+  ReducePlan p;
+  plan_reduce(p, ndim, in_shape, in_strides, axis, axis_len, out_size);
+  return tiles_hint(p, elem_size);
+}
+
+// value reductions whose final step is the plain accumulator (sum/prod/max/min, real + complex)
+#define MPY_RED_FAMILY(NAME, OP, SN, T)                                                                     \
+  void musapy_##NAME##_##SN##_v2(const T* a, T* c, RED_ARGS, hipStream_t st) {                              \
+    launch_reduce<OP<T>, T, kWriteFinal>(a, vout<T>(c), RED_PASS, 1, st);                                   \
+  }                                                                                                         \
+  void musapy_##NAME##_small_axis_##SN##_v2(const T* a, T* c, RED_ARGS, int group_size, hipStream_t st) {   \
+    (void)group_size;                                                                                       \
+    launch_reduce<OP<T>, T, kWriteFinal>(a, vout<T>(c), RED_PASS, 1, st);                                   \
+  }                                                                                                         \
+  void musapy_##NAME##_partial_##SN##_v2(const T* a, T* partials, RED_ARGS, size_t tiles_per_output,        \
+                                         hipStream_t st) {                                                  \
+    launch_reduce<OP<T>, T, kWriteVal>(a, vout<T>(partials), RED_PASS, tiles_per_output, st);               \
+  }
+
+#define MPY_RED_FINAL_REAL(NAME, OP, SN, T)                                                                 \
+  void musapy_##NAME##_final_##SN##_v2(const T* partials, T* c, size_t num_partials, size_t out_size,       \
+                                       hipStream_t st) {                                                    \
+    launch_final<OP<T>, T>(partials, vout<T>(c), num_partials, out_size, st);                               \
+  }
+#define MPY_RED_FINAL_CPLX(NAME, OP, SN, T)                                                                 \
+  void musapy_##NAME##_final_##SN##_v2(const T* partials, T* c, size_t num_partials, size_t out_size,       \
+                                       size_t axis_len, hipStream_t st) {                                   \
+    (void)axis_len;                                                                                         \
+    launch_final<OP<T>, T>(partials, vout<T>(c), num_partials, out_size, st);                               \
+  }
+
+#define MPY_RED_REAL(SN, T)                  \
+  MPY_RED_FAMILY(sum, OpSum, SN, T)          \
+  MPY_RED_FAMILY(prod, OpProd, SN, T)        \
+  MPY_RED_FAMILY(max, OpMax, SN, T)          \
+  MPY_RED_FAMILY(min, OpMin, SN, T)          \
+  MPY_RED_FINAL_REAL(sum, OpSum, SN, T)      \
+  MPY_RED_FINAL_REAL(prod, OpProd, SN, T)    \
+  MPY_RED_FINAL_REAL(max, OpMax, SN, T)      \
+  MPY_RED_FINAL_REAL(min, OpMin, SN, T)
+MPY_RED_REAL(i64, int64_t)
+MPY_RED_REAL(f32, float)
+MPY_RED_REAL(f64, double)
+
+#define MPY_RED_CPLX(SN, T)                  \
+  MPY_RED_FAMILY(sum, OpSum, SN, T)          \
+  MPY_RED_FAMILY(prod, OpProd, SN, T)        \
+  MPY_RED_FINAL_CPLX(sum, OpSum, SN, T)      \
+  MPY_RED_FINAL_CPLX(prod, OpProd, SN, T)
+MPY_RED_CPLX(c64, musapy_c64_t)
+MPY_RED_CPLX(c128, musapy_c128_t)
+
+// mean: sum partials, divide in the final step.  Real means divide by the reference's "+1"
+// count in T (cpu_mean_typed, op_builder.rs:3608-3612); complex means by the f64 axis length
+// (cpu_reduce_cplx, op_builder.rs:3485-3488).
+#define MPY_RED_MEAN(SN, T, COUNT)                                                                          \
+  void musapy_mean_##SN##_v2(const T* a, T* c, RED_ARGS, hipStream_t st) {                                  \
+    launch_reduce<OpSum<T>, T, kWriteFinal>(a, mout<T>(c, COUNT(axis_len)), RED_PASS, 1, st);               \
+  }                                                                                                         \
+  void musapy_mean_small_axis_##SN##_v2(const T* a, T* c, RED_ARGS, int group_size, hipStream_t st) {       \
+    (void)group_size;                                                                                       \
+    launch_reduce<OpSum<T>, T, kWriteFinal>(a, mout<T>(c, COUNT(axis_len)), RED_PASS, 1, st);               \
+  }                                                                                                         \
+  void musapy_mean_partial_##SN##_v2(const T* a, T* partials, RED_ARGS, size_t tiles_per_output,            \
+                                     hipStream_t st) {                                                      \
+    launch_reduce<OpSum<T>, T, kWriteVal>(a, vout<T>(partials), RED_PASS, tiles_per_output, st);            \
+  }                                                                                                         \
+  void musapy_mean_final_##SN##_v2(const T* partials, T* c, size_t num_partials, size_t out_size,           \
+                                   size_t axis_len, hipStream_t st) {                                       \
+    launch_final<OpSum<T>, T>(partials, mout<T>(c, COUNT(axis_len)), num_partials, out_size, st);           \
+  }
+#define MPY_COUNT_F32(n) mean_count<float>(n)
+#define MPY_COUNT_F64(n) mean_count<double>(n)
+#define MPY_COUNT_LEN(n) double(n)
+MPY_RED_MEAN(f32, float, MPY_COUNT_F32)
+MPY_RED_MEAN(f64, double, MPY_COUNT_F64)
+MPY_RED_MEAN(c64, musapy_c64_t, MPY_COUNT_LEN)
+MPY_RED_MEAN(c128, musapy_c128_t, MPY_COUNT_LEN)
+
+// argmax / argmin
+#define MPY_RED_ARG(NAME, OP, SN, T)                                                                        \
+  void musapy_##NAME##_##SN##_v2(const T* a, int64_t* c, RED_ARGS, hipStream_t st) {                        \
+    launch_reduce<OP<T>, T, kWriteFinal>(a, iout<T>(c), RED_PASS, 1, st);                                   \
+  }                                                                                                         \
+  void musapy_##NAME##_partial_##SN##_v2(const T* a, T* partials_val, int64_t* partials_idx, RED_ARGS,      \
+                                         size_t tiles_per_output, hipStream_t st) {                         \
+    RedOut<T> o{partials_val, partials_idx, 0.0, kFinPlain};                                                \
+    launch_reduce<OP<T>, T, kWritePair>(a, o, RED_PASS, tiles_per_output, st);                              \
+  }                                                                                                         \
+  void musapy_##NAME##_final_##SN##_v2(const T* partials_val, const int64_t* partials_idx, int64_t* c,      \
+                                       size_t num_partials, size_t out_size, hipStream_t st) {              \
+    launch_pairs<OP<T>, T, kWriteFinal>(partials_val, partials_idx, iout<T>(c), num_partials, out_size, 1,  \
+                                        st);                                                                \
+  }                                                                                                         \
+  void musapy_##NAME##_mid_##SN##_v2(const T* partials_val, const int64_t* partials_idx, T* out_val,        \
+                                     int64_t* out_idx, size_t out_size, size_t tiles_per_output,            \
+                                     size_t axis_len, hipStream_t st) {                                     \
+    RedOut<T> o{out_val, out_idx, 0.0, kFinPlain};                                                          \
+    launch_pairs<OP<T>, T, kWritePair>(partials_val, partials_idx, o, axis_len, out_size, tiles_per_output, \
+                                       st);                                                                 \
+  }
+MPY_RED_ARG(argmax, OpArgmax, i64, int64_t)
+MPY_RED_ARG(argmax, OpArgmax, f32, float)
+MPY_RED_ARG(argmax, OpArgmax, f64, double)
+MPY_RED_ARG(argmin, OpArgmin, i64, int64_t)
+MPY_RED_ARG(argmin, OpArgmin, f32, float)
+MPY_RED_ARG(argmin, OpArgmin, f64, double)
+
+}  // extern "C"

@@ -1,0 +1,726 @@
+// ops.cpp -- the op builder: three-phase elementwise / cast / reduction / scan operators.
+//
+// Ports the control flow of rust/musapy-ops/src/op_builder.rs (binary_elementwise 315-532,
+// unary_elementwise 550-732, clamp_elementwise 740-891, validate_cast_pair 904-962,
+// cast_array 1055-1119, astype_op 1130-1292, reduction_axis 2310-3139, cumsum_op 3144-3363),
+// rust/musapy-ops/src/reduction.rs (axis resolution, reduce_multi, arg_reduce_multi) and
+// rust/musapy-ops/src/broadcast.rs.  Phase B only calls the C kernel ABI; there is no host
+// compute path.  Path selection for reductions differs from the reference (which switches on
+// axis_len thresholds, op_builder.rs:2513-2514): the kernel library reports how many tiles per
+// output a reduction needs to fill the GPU (musapy_reduce_tiles_hint) and the op layer uses the
+// single-pass entry point when that is 1, partial + final otherwise.
+#include "ops.hpp"
+
+#include <algorithm>
+
+#include "../../../include/musapy_kernels.h"
+#include "../../../include/musapy_hip_runtime.h"
+
+extern "C" {
+// copy kernels (rust/musapy-ops/src/kernels.rs:321-324 signature; u8/u16 are new)
+void musapy_copy_f32(const float* input, float* output, int ndim, const size_t* shape, const ssize_t* in_strides,
+                     hipStream_t stream);
+void musapy_copy_f64(const double* input, double* output, int ndim, const size_t* shape, const ssize_t* in_strides,
+                     hipStream_t stream);
+void musapy_copy_i32(const int32_t* input, int32_t* output, int ndim, const size_t* shape, const ssize_t* in_strides,
+                     hipStream_t stream);
+void musapy_copy_i64(const int64_t* input, int64_t* output, int ndim, const size_t* shape,
+                     const ssize_t* in_strides, hipStream_t stream);
+void musapy_copy_u8(const uint8_t* input, uint8_t* output, int ndim, const size_t* shape, const ssize_t* in_strides,
+                    hipStream_t stream);
+void musapy_copy_u16(const uint16_t* input, uint16_t* output, int ndim, const size_t* shape,
+                     const ssize_t* in_strides, hipStream_t stream);
+}
+
+namespace mpy {
+namespace ops {
+
+namespace {
+
+const char* bname(BinaryKernel k) {
+  static const char* n[] = {"add", "sub", "mul", "div", "pow"};
+  return n[int(k)];
+}
+const char* uname(UnaryKernel k) {
+  static const char* n[] = {"sin", "cos", "exp", "log", "abs", "sign", "neg"};
+  return n[int(k)];
+}
+const char* rname(ReduceKernel k) {
+  static const char* n[] = {"sum", "prod", "max", "min", "mean", "argmax", "argmin"};
+  return n[int(k)];
+}
+
+void check_out(const char* op, const Array* out, const Shape& shape, Dtype dtype, const Array& a,
+               const char* shape_what, const char* dtype_what) {
+  if (!out) return;
+  auto fmt = [](const Shape& s) {
+    std::string r = "[";
+    for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+    return r + "]";
+  };
+  if (out->shape() != shape)
+    throw ShapeError(std::string(op) + ": out shape " + fmt(out->shape()) + " != " + shape_what + " " + fmt(shape));
+  if (out->dtype != dtype)
+    throw DtypeError(std::string(op) + ": out dtype " + dtype_name(out->dtype) + " != " + dtype_what + " " +
+                     dtype_name(dtype));
+  if (out->device != a.device)
+    throw DeviceError(std::string(op) + ": out device hip:" + std::to_string(out->device) + " != input device hip:" +
+                      std::to_string(a.device));
+}
+
+// Allocates the output (or adopts out=) and runs the alias check (op_builder.rs:420-433).
+Array make_output(const Array* out, const Shape& shape, Dtype dtype, int device, const StreamPtr& s,
+                  std::initializer_list<const Array*> inputs) {
+  if (out) {
+    if (!out->layout.has_contiguous_strides()) throw ShapeError("out= must have C-contiguous strides");
+    for (const Array* in : inputs)
+      if (in && out->data.get() == in->data.get())
+        throw MemoryError("alias detected: out= shares its buffer with an input");
+    out->data->wait_reads_on(s);
+    Array r = *out;
+    r.stream = s;
+    return r;
+  }
+  return new_array(shape, dtype, device, s);
+}
+
+std::vector<size_t> shape_vec(const Shape& s) { return s; }
+
+}  // namespace
+
+StreamPtr pick_stream(const Array& a, const Array* out) {
+  if (out) return out->stream;
+  StreamPtr cur = current_stream();
+  return cur ? cur : a.stream;
+}
+
+// ---------------------------------------------------------------------------------------------
+// broadcast.rs:24-92
+Shape broadcast_shape(const std::vector<Shape>& shapes) {
+  size_t nd = 0;
+  for (auto& s : shapes) nd = std::max(nd, s.size());
+  Shape r(nd, 1);
+  for (auto& s : shapes) {
+    size_t off = nd - s.size();
+    for (size_t i = 0; i < s.size(); ++i) {
+      size_t o = off + i;
+      if (r[o] == 1)
+        r[o] = s[i];
+      else if (s[i] != 1 && s[i] != r[o])
+        throw ShapeError("broadcast: incompatible shapes (dim " + std::to_string(o) + " = " + std::to_string(r[o]) +
+                         " vs " + std::to_string(s[i]) + ")");
+    }
+  }
+  return r;
+}
+
+Strides broadcast_strides(const Layout& layout, const Shape& target) {
+  size_t nd = target.size();
+  Strides r(nd, 0);
+  size_t off = nd >= layout.ndim() ? nd - layout.ndim() : 0;
+  for (size_t i = 0; i < layout.ndim(); ++i) {
+    size_t o = off + i;
+    if (o >= nd) break;
+    if (layout.shape[i] == target[o]) r[o] = layout.strides[i];
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// casts -- op_builder.rs:904-962 plus the new f32 -> f16 / bf16 pairs
+void validate_cast_pair(Dtype src, Dtype dst) {
+  bool new_pair = src == Dtype::Float32 && (dst == Dtype::Float16 || dst == Dtype::Bfloat16);
+  if (new_pair) return;
+  switch (src) {
+    case Dtype::Int8: case Dtype::Int16: case Dtype::Int32: case Dtype::Int64:
+    case Dtype::Uint8: case Dtype::Uint16: case Dtype::Uint32: case Dtype::Uint64:
+    case Dtype::Float32: case Dtype::Float64:
+      break;
+    case Dtype::Complex64: case Dtype::Complex128:
+      throw DtypeError(std::string("cast: ") + dtype_name(src) + " -> " + dtype_name(dst) +
+                       " not supported (complex casts are outside this backend's path)");
+    default:
+      throw DtypeError(std::string("cast: source dtype ") + dtype_name(src) +
+                       " not supported (bool/float16/bfloat16 sources have no cast kernel)");
+  }
+  switch (dst) {
+    case Dtype::Float32: case Dtype::Float64: case Dtype::Int64: break;
+    case Dtype::Complex64: case Dtype::Complex128:
+      throw DtypeError(std::string("cast: ") + dtype_name(src) + " -> " + dtype_name(dst) +
+                       " not supported (real->complex casts are outside this backend's path)");
+    default:
+      throw DtypeError(std::string("cast: target dtype ") + dtype_name(dst) +
+                       " not supported (only float32/float64/int64, and float16/bfloat16 from float32)");
+  }
+  if (src == dst) throw DtypeError(std::string("cast: source and target dtype are identical (") + dtype_name(src) + ")");
+}
+
+namespace {
+
+void launch_cast(const void* a, void* c, const Shape& shape, const Strides& st, Dtype src, Dtype dst,
+                 hipStream_t s) {
+  if (shape_numel(shape) == 0) return;
+  const int nd = int(shape.size());
+  const size_t* sh = shape.data();
+  const ssize_t* ss = st.data();
+#define CAST_CASE(SD, ST, FN, DT) \
+  case Dtype::SD: FN((const ST*)a, (DT*)c, nd, sh, ss, s); break;
+  if (dst == Dtype::Float32) {
+    switch (src) {
+      CAST_CASE(Int8, int8_t, musapy_cast_i8_f32_v2, float)
+      CAST_CASE(Int16, int16_t, musapy_cast_i16_f32_v2, float)
+      CAST_CASE(Int32, int32_t, musapy_cast_i32_f32_v2, float)
+      CAST_CASE(Int64, int64_t, musapy_cast_i64_f32_v2, float)
+      CAST_CASE(Uint8, uint8_t, musapy_cast_u8_f32_v2, float)
+      CAST_CASE(Uint16, uint16_t, musapy_cast_u16_f32_v2, float)
+      CAST_CASE(Uint32, uint32_t, musapy_cast_u32_f32_v2, float)
+      CAST_CASE(Uint64, uint64_t, musapy_cast_u64_f32_v2, float)
+      CAST_CASE(Float64, double, musapy_cast_f64_f32_v2, float)
+      default: throw DtypeError("cast pair not validated");
+    }
+  } else if (dst == Dtype::Float64) {
+    switch (src) {
+      CAST_CASE(Int8, int8_t, musapy_cast_i8_f64_v2, double)
+      CAST_CASE(Int16, int16_t, musapy_cast_i16_f64_v2, double)
+      CAST_CASE(Int32, int32_t, musapy_cast_i32_f64_v2, double)
+      CAST_CASE(Int64, int64_t, musapy_cast_i64_f64_v2, double)
+      CAST_CASE(Uint8, uint8_t, musapy_cast_u8_f64_v2, double)
+      CAST_CASE(Uint16, uint16_t, musapy_cast_u16_f64_v2, double)
+      CAST_CASE(Uint32, uint32_t, musapy_cast_u32_f64_v2, double)
+      CAST_CASE(Uint64, uint64_t, musapy_cast_u64_f64_v2, double)
+      CAST_CASE(Float32, float, musapy_cast_f32_f64_v2, double)
+      default: throw DtypeError("cast pair not validated");
+    }
+  } else if (dst == Dtype::Int64) {
+    switch (src) {
+      CAST_CASE(Int8, int8_t, musapy_cast_i8_i64_v2, int64_t)
+      CAST_CASE(Int16, int16_t, musapy_cast_i16_i64_v2, int64_t)
+      CAST_CASE(Int32, int32_t, musapy_cast_i32_i64_v2, int64_t)
+      CAST_CASE(Uint8, uint8_t, musapy_cast_u8_i64_v2, int64_t)
+      CAST_CASE(Uint16, uint16_t, musapy_cast_u16_i64_v2, int64_t)
+      CAST_CASE(Uint32, uint32_t, musapy_cast_u32_i64_v2, int64_t)
+      CAST_CASE(Uint64, uint64_t, musapy_cast_u64_i64_v2, int64_t)
+      CAST_CASE(Float32, float, musapy_cast_f32_i64_v2, int64_t)
+      CAST_CASE(Float64, double, musapy_cast_f64_i64_v2, int64_t)
+      default: throw DtypeError("cast pair not validated");
+    }
+  } else if (dst == Dtype::Bfloat16 && src == Dtype::Float32) {
+    musapy_cast_f32_bf16_v2((const float*)a, (uint16_t*)c, nd, sh, ss, s);
+  } else if (dst == Dtype::Float16 && src == Dtype::Float32) {
+    musapy_cast_f32_f16_v2((const float*)a, (uint16_t*)c, nd, sh, ss, s);
+  } else {
+    throw DtypeError("cast pair not validated");
+  }
+#undef CAST_CASE
+  check_launch("cast");
+}
+
+}  // namespace
+
+Array cast_array(const Array& a, Dtype target, const StreamPtr& stream) {
+  validate_cast_pair(a.dtype, target);
+  Array out = new_array(a.shape(), target, a.device, stream);
+  a.data->wait_last_write_on(stream);
+  launch_cast(a.data_ptr(), out.data->ptr(), a.shape(), a.layout.strides, a.dtype, target, stream->raw());
+  a.data->record_read(stream);
+  out.data->record_write(stream);
+  return out;
+}
+
+Array astype_op(const Array& a, Dtype dtype, const Array* out) {
+  if (a.dtype != dtype) validate_cast_pair(a.dtype, dtype);
+  check_out("astype", out, a.shape(), dtype, a, "input shape", "target dtype");
+  StreamPtr s = pick_stream(a, out);
+  Array r = make_output(out, a.shape(), dtype, a.device, s, {&a});
+  a.data->wait_last_write_on(s);
+  if (a.size() > 0) {
+    if (a.dtype == dtype) {
+      if (!a.is_contiguous())
+        throw DtypeError("astype: same-dtype copy requires contiguous input (reference limitation kept)");
+      check_rt(mpy_rt_memcpy_d2d(r.data->ptr(), a.data_ptr(), a.nbytes(), s->raw()), "astype copy");
+    } else {
+      launch_cast(a.data_ptr(), r.data_ptr(), a.shape(), a.layout.strides, a.dtype, dtype, s->raw());
+    }
+  }
+  a.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// elementwise
+Array binary_elementwise(const Array& a, const Array& b, const Array* out, BinaryKernel k) {
+  const char* op = bname(k);
+  if (a.device != b.device)
+    throw DeviceError(std::string(op) + ": device mismatch hip:" + std::to_string(a.device) + " vs hip:" +
+                      std::to_string(b.device));
+  Shape out_shape = broadcast_shape({a.shape(), b.shape()});
+  Dtype dt = promote(a.dtype, b.dtype, /*all_gpu=*/true);
+  if (dt != Dtype::Float32 && dt != Dtype::Float64) {
+    if (is_complex(dt))
+      throw DtypeError(std::string(op) + ": complex elementwise arithmetic is outside this backend's path");
+    throw DtypeError(std::string(op) + ": promoted dtype " + dtype_name(dt) +
+                     " not supported (compute whitelist: float32/float64)");
+  }
+  check_out(op, out, out_shape, dt, a, "broadcast output shape", "promoted dtype");
+  StreamPtr s = pick_stream(a, out);
+  std::optional<Array> ac, bc;
+  if (a.dtype != dt) ac = cast_array(a, dt, s);
+  if (b.dtype != dt) bc = cast_array(b, dt, s);
+  const Array& aw = ac ? *ac : a;
+  const Array& bw = bc ? *bc : b;
+  Array r = make_output(out, out_shape, dt, a.device, s, {&aw, &bw});
+  aw.data->wait_last_write_on(s);
+  bw.data->wait_last_write_on(s);
+  if (shape_numel(out_shape) > 0) {
+    Strides as = aw.shape() == out_shape ? aw.layout.strides : broadcast_strides(aw.layout, out_shape);
+    Strides bs = bw.shape() == out_shape ? bw.layout.strides : broadcast_strides(bw.layout, out_shape);
+    const int nd = int(out_shape.size());
+#define BIN(T, SFX)                                                                                         \
+  {                                                                                                         \
+    auto fn = k == BinaryKernel::Add ? musapy_add_##SFX##_v2                                                \
+              : k == BinaryKernel::Sub ? musapy_sub_##SFX##_v2                                              \
+              : k == BinaryKernel::Mul ? musapy_mul_##SFX##_v2                                              \
+              : k == BinaryKernel::Div ? musapy_div_##SFX##_v2                                              \
+                                       : musapy_pow_##SFX##_v2;                                             \
+    fn((const T*)aw.data_ptr(), (const T*)bw.data_ptr(), (T*)r.data_ptr(), nd, out_shape.data(), as.data(), \
+       bs.data(), s->raw());                                                                                \
+  }
+    if (dt == Dtype::Float32) BIN(float, f32) else BIN(double, f64)
+#undef BIN
+    check_launch(op);
+  }
+  aw.data->record_read(s);
+  bw.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+Array unary_elementwise(const Array& a, const Array* out, UnaryKernel k) {
+  const char* op = uname(k);
+  Dtype dt = a.dtype;
+  if (dt != Dtype::Float32 && dt != Dtype::Float64) {
+    if (is_complex(dt))
+      throw DtypeError(std::string(op) + ": complex elementwise ops are outside this backend's path");
+    throw DtypeError(std::string(op) + ": dtype " + dtype_name(dt) + " not supported (only float32/float64)");
+  }
+  check_out(op, out, a.shape(), dt, a, "input shape", "expected output dtype");
+  StreamPtr s = pick_stream(a, out);
+  Array r = make_output(out, a.shape(), dt, a.device, s, {&a});
+  a.data->wait_last_write_on(s);
+  if (a.size() > 0) {
+    const int nd = int(a.ndim());
+#define UN(T, SFX)                                                                                               \
+  {                                                                                                              \
+    auto fn = k == UnaryKernel::Sin ? musapy_sin_##SFX##_v2                                                      \
+              : k == UnaryKernel::Cos ? musapy_cos_##SFX##_v2                                                    \
+              : k == UnaryKernel::Exp ? musapy_exp_##SFX##_v2                                                    \
+              : k == UnaryKernel::Log ? musapy_log_##SFX##_v2                                                    \
+              : k == UnaryKernel::Abs ? musapy_abs_##SFX##_v2                                                    \
+              : k == UnaryKernel::Sign ? musapy_sign_##SFX##_v2                                                  \
+                                       : musapy_neg_##SFX##_v2;                                                  \
+    fn((const T*)a.data_ptr(), (T*)r.data_ptr(), nd, a.shape().data(), a.layout.strides.data(), s->raw());      \
+  }
+    if (dt == Dtype::Float32) UN(float, f32) else UN(double, f64)
+#undef UN
+    check_launch(op);
+  }
+  a.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+Array clamp_elementwise(const Array& a, double lo, double hi, const Array* out) {
+  Dtype dt = a.dtype;
+  if (dt != Dtype::Float32 && dt != Dtype::Float64)
+    throw DtypeError(std::string("clamp: dtype ") + dtype_name(dt) + " not supported (only float32/float64)");
+  check_out("clamp", out, a.shape(), dt, a, "input shape", "input dtype");
+  StreamPtr s = pick_stream(a, out);
+  Array r = make_output(out, a.shape(), dt, a.device, s, {&a});
+  a.data->wait_last_write_on(s);
+  if (a.size() > 0) {
+    const int nd = int(a.ndim());
+    if (dt == Dtype::Float32)  // lo/hi narrowed like op_builder.rs:850-853
+      musapy_clamp_f32_v2((const float*)a.data_ptr(), (float*)r.data_ptr(), float(lo), float(hi), nd,
+                          a.shape().data(), a.layout.strides.data(), s->raw());
+    else
+      musapy_clamp_f64_v2((const double*)a.data_ptr(), (double*)r.data_ptr(), lo, hi, nd, a.shape().data(),
+                          a.layout.strides.data(), s->raw());
+    check_launch("clamp");
+  }
+  a.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// reductions
+namespace {
+
+// op_builder.rs:2209-2225
+Dtype reduction_compute_dtype(Dtype in, ReduceKernel k) {
+  if (in == Dtype::Float32 || in == Dtype::Float64) return in;
+  if (is_complex(in)) return in;
+  return k == ReduceKernel::Mean ? Dtype::Float64 : Dtype::Int64;
+}
+
+bool is_arg(ReduceKernel k) { return k == ReduceKernel::Argmax || k == ReduceKernel::Argmin; }
+
+struct RedCall {
+  const void* a;
+  int nd;
+  const size_t* shape;
+  const ssize_t* strides;
+  int axis;
+  size_t axis_len, out_size;
+  hipStream_t s;
+};
+
+#define RED_CALL_ARGS c.nd, c.shape, c.strides, c.axis, c.axis_len, c.out_size
+
+void red_single(ReduceKernel k, Dtype ct, const RedCall& c, void* out) {
+#define R1(OP, SFX, T, OT) musapy_##OP##_##SFX##_v2((const T*)c.a, (OT*)out, RED_CALL_ARGS, c.s)
+#define RREAL(SFX, T)                                                   \
+  switch (k) {                                                          \
+    case ReduceKernel::Sum: R1(sum, SFX, T, T); break;                  \
+    case ReduceKernel::Prod: R1(prod, SFX, T, T); break;                \
+    case ReduceKernel::Max: R1(max, SFX, T, T); break;                  \
+    case ReduceKernel::Min: R1(min, SFX, T, T); break;                  \
+    case ReduceKernel::Argmax: R1(argmax, SFX, T, int64_t); break;      \
+    case ReduceKernel::Argmin: R1(argmin, SFX, T, int64_t); break;      \
+    default: throw DtypeError("reduction not available for dtype");     \
+  }
+  switch (ct) {
+    case Dtype::Int64: RREAL(i64, int64_t) break;
+    case Dtype::Float32:
+      if (k == ReduceKernel::Mean) R1(mean, f32, float, float); else RREAL(f32, float)
+      break;
+    case Dtype::Float64:
+      if (k == ReduceKernel::Mean) R1(mean, f64, double, double); else RREAL(f64, double)
+      break;
+    case Dtype::Complex64:
+      if (k == ReduceKernel::Sum) R1(sum, c64, musapy_c64_t, musapy_c64_t);
+      else if (k == ReduceKernel::Prod) R1(prod, c64, musapy_c64_t, musapy_c64_t);
+      else R1(mean, c64, musapy_c64_t, musapy_c64_t);
+      break;
+    case Dtype::Complex128:
+      if (k == ReduceKernel::Sum) R1(sum, c128, musapy_c128_t, musapy_c128_t);
+      else if (k == ReduceKernel::Prod) R1(prod, c128, musapy_c128_t, musapy_c128_t);
+      else R1(mean, c128, musapy_c128_t, musapy_c128_t);
+      break;
+    default: throw DtypeError("reduction compute dtype not supported");
+  }
+#undef RREAL
+#undef R1
+}
+
+// partial -> final for value reductions (sum/prod/max/min/mean)
+void red_two_stage(ReduceKernel k, Dtype ct, const RedCall& c, void* out, size_t tiles, void* partials) {
+#define P2(OP, SFX, T) musapy_##OP##_partial_##SFX##_v2((const T*)c.a, (T*)partials, RED_CALL_ARGS, tiles, c.s)
+#define F2(OP, SFX, T) musapy_##OP##_final_##SFX##_v2((const T*)partials, (T*)out, tiles, c.out_size, c.s)
+#define F2L(OP, SFX, T) musapy_##OP##_final_##SFX##_v2((const T*)partials, (T*)out, tiles, c.out_size, c.axis_len, c.s)
+#define V2(SFX, T)                                                       \
+  switch (k) {                                                           \
+    case ReduceKernel::Sum: P2(sum, SFX, T); F2(sum, SFX, T); break;     \
+    case ReduceKernel::Prod: P2(prod, SFX, T); F2(prod, SFX, T); break;  \
+    case ReduceKernel::Max: P2(max, SFX, T); F2(max, SFX, T); break;     \
+    case ReduceKernel::Min: P2(min, SFX, T); F2(min, SFX, T); break;     \
+    default: throw DtypeError("reduction not available for dtype");      \
+  }
+  switch (ct) {
+    case Dtype::Int64: V2(i64, int64_t) break;
+    case Dtype::Float32:
+      if (k == ReduceKernel::Mean) { P2(mean, f32, float); F2L(mean, f32, float); } else V2(f32, float)
+      break;
+    case Dtype::Float64:
+      if (k == ReduceKernel::Mean) { P2(mean, f64, double); F2L(mean, f64, double); } else V2(f64, double)
+      break;
+    case Dtype::Complex64:
+      if (k == ReduceKernel::Sum) { P2(sum, c64, musapy_c64_t); F2L(sum, c64, musapy_c64_t); }
+      else if (k == ReduceKernel::Prod) { P2(prod, c64, musapy_c64_t); F2L(prod, c64, musapy_c64_t); }
+      else { P2(mean, c64, musapy_c64_t); F2L(mean, c64, musapy_c64_t); }
+      break;
+    case Dtype::Complex128:
+      if (k == ReduceKernel::Sum) { P2(sum, c128, musapy_c128_t); F2L(sum, c128, musapy_c128_t); }
+      else if (k == ReduceKernel::Prod) { P2(prod, c128, musapy_c128_t); F2L(prod, c128, musapy_c128_t); }
+      else { P2(mean, c128, musapy_c128_t); F2L(mean, c128, musapy_c128_t); }
+      break;
+    default: throw DtypeError("reduction compute dtype not supported");
+  }
+#undef V2
+#undef F2L
+#undef F2
+#undef P2
+}
+
+void red_arg_two_stage(ReduceKernel k, Dtype ct, const RedCall& c, int64_t* out, size_t tiles, void* pv,
+                       int64_t* pi) {
+#define A2(OP, SFX, T)                                                                          \
+  musapy_##OP##_partial_##SFX##_v2((const T*)c.a, (T*)pv, pi, RED_CALL_ARGS, tiles, c.s);       \
+  musapy_##OP##_final_##SFX##_v2((const T*)pv, pi, out, tiles, c.out_size, c.s);
+#define AA(SFX, T) \
+  if (k == ReduceKernel::Argmax) { A2(argmax, SFX, T) } else { A2(argmin, SFX, T) }
+  switch (ct) {
+    case Dtype::Int64: AA(i64, int64_t) break;
+    case Dtype::Float32: AA(f32, float) break;
+    case Dtype::Float64: AA(f64, double) break;
+    default: throw DtypeError("arg reduction compute dtype not supported");
+  }
+#undef AA
+#undef A2
+}
+
+}  // namespace
+
+std::optional<size_t> resolve_axis(std::optional<ssize_t> axis, size_t ndim) {
+  if (!axis) return std::nullopt;
+  ssize_t ax = *axis, n = ssize_t(ndim);
+  ssize_t norm = ax < 0 ? ax + n : ax;
+  if (norm < 0 || norm >= n)
+    throw ShapeError("axis " + std::to_string(ax) + " is out of bounds for array of dimension " + std::to_string(ndim));
+  return size_t(norm);
+}
+
+std::vector<size_t> resolve_axes(const std::vector<ssize_t>* axes, size_t ndim) {
+  std::vector<size_t> r;
+  if (!axes) return r;
+  for (ssize_t ax : *axes) r.push_back(*resolve_axis(ax, ndim));
+  std::sort(r.begin(), r.end());
+  for (size_t i = 1; i < r.size(); ++i)
+    if (r[i] == r[i - 1]) throw ShapeError("duplicate value in 'axis' argument: " + std::to_string(r[i]));
+  return r;
+}
+
+Array reduction_axis(const Array& a, std::optional<size_t> axis, bool keepdims, const Array* out, ReduceKernel k) {
+  const char* op = rname(k);
+  if (is_complex(a.dtype) && (k == ReduceKernel::Max || k == ReduceKernel::Min || is_arg(k)))
+    throw DtypeError(std::string(op) + ": ordering reduction not supported for complex dtype " + dtype_name(a.dtype) +
+                     " (complex has no total order)");
+  const Shape in_shape = a.shape();
+  const size_t nd = in_shape.size();
+  Shape out_shape;
+  if (!axis) {
+    if (keepdims) out_shape.assign(nd, 1);
+  } else {
+    for (size_t i = 0; i < nd; ++i) {
+      if (i == *axis) {
+        if (keepdims) out_shape.push_back(1);
+      } else {
+        out_shape.push_back(in_shape[i]);
+      }
+    }
+  }
+  Dtype ct = reduction_compute_dtype(a.dtype, k);
+  Dtype out_dt = is_arg(k) ? Dtype::Int64 : ct;
+  const size_t total = shape_numel(in_shape);
+  Shape kshape = axis ? in_shape : Shape{total};
+  const int kaxis = axis ? int(*axis) : 0;
+  const size_t axis_len = axis ? in_shape[*axis] : total;
+  const size_t out_size = std::max<size_t>(shape_numel(out_shape), 1);
+  check_out(op, out, out_shape, out_dt, a, "expected output shape", "expected");
+  StreamPtr s = pick_stream(a, out);
+  std::optional<Array> cast;
+  if (a.dtype != ct) cast = cast_array(a, ct, s);
+  const Array* aw = cast ? &*cast : &a;
+  Array r = make_output(out, out_shape, out_dt, a.device, s, {aw});
+  aw->data->wait_last_write_on(s);
+  std::optional<Array> flat;
+  if (!axis && !aw->layout.has_contiguous_strides()) {
+    flat = contiguous(*aw);
+    flat->data->wait_last_write_on(s);
+    aw = &*flat;
+  }
+  if (axis_len == 0 && shape_numel(out_shape) > 0 &&
+      (k == ReduceKernel::Max || k == ReduceKernel::Min || is_arg(k)))
+    throw ShapeError(std::string(op) + ": zero-size reduction has no identity");
+  if (out_size > 0 && shape_numel(out_shape.empty() ? Shape{1} : out_shape) > 0) {
+    Strides kstrides = axis ? aw->layout.strides : Strides{1};
+    RedCall c{aw->data_ptr(), int(kshape.size()), kshape.data(), kstrides.data(), kaxis, axis_len, out_size, s->raw()};
+    const size_t es = element_size(ct);
+    size_t tiles = axis_len == 0 ? 1
+                                 : musapy_reduce_tiles_hint(c.nd, c.shape, c.strides, c.axis, axis_len, out_size, es);
+    if (tiles <= 1) {
+      red_single(k, ct, c, r.data_ptr());
+    } else if (is_arg(k)) {
+      BufferRef pv = Buffer::alloc(out_size * tiles * es, a.device, s);
+      BufferRef pi = Buffer::alloc(out_size * tiles * 8, a.device, s);
+      red_arg_two_stage(k, ct, c, (int64_t*)r.data_ptr(), tiles, pv->ptr(), (int64_t*)pi->ptr());
+    } else {
+      BufferRef pp = Buffer::alloc(out_size * tiles * es, a.device, s);
+      red_two_stage(k, ct, c, r.data_ptr(), tiles, pp->ptr());
+    }
+    check_launch(op);
+  }
+  aw->data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+// reduction.rs:118-155
+Array reduce_multi(const Array& a, const std::vector<ssize_t>* axes, bool keepdims, const Array* out,
+                   ReduceKernel k) {
+  std::vector<size_t> ax = resolve_axes(axes, a.ndim());
+  if (ax.empty()) return reduction_axis(a, std::nullopt, keepdims, out, k);
+  if (ax.size() == 1) return reduction_axis(a, ax[0], keepdims, out, k);
+  if (out) throw ShapeError("reduction with multiple axes does not support out= yet");
+  std::optional<Array> cur;
+  for (size_t x : ax) cur = reduction_axis(cur ? *cur : a, x, true, nullptr, k);
+  if (keepdims) return *cur;
+  Array res = *cur;
+  for (size_t i = 0; i < ax.size(); ++i) res = index_select(res, ax[i] - i, 0);
+  return res;
+}
+
+// reduction.rs:186-226
+Array arg_reduce_multi(const Array& a, const std::vector<ssize_t>* axes, bool keepdims, const Array* out,
+                       ReduceKernel k) {
+  std::vector<size_t> ax = resolve_axes(axes, a.ndim());
+  if (ax.empty()) return reduction_axis(a, std::nullopt, keepdims, out, k);
+  if (ax.size() == 1) return reduction_axis(a, ax[0], keepdims, out, k);
+  const size_t nd = a.ndim();
+  std::vector<size_t> perm;
+  for (size_t i = 0; i < nd; ++i)
+    if (std::find(ax.begin(), ax.end(), i) == ax.end()) perm.push_back(i);
+  perm.insert(perm.end(), ax.begin(), ax.end());
+  Array t = transpose(a, &perm);
+  Array cont = contiguous(t);
+  Array merged = reshape_merge_last(cont, ax.size());
+  Array res = reduction_axis(merged, merged.ndim() - 1, keepdims, out, k);
+  if (!keepdims) return res;
+  Array split = reshape_split_last(res, ax.size());
+  std::vector<size_t> inv(nd);
+  for (size_t i = 0; i < nd; ++i) inv[perm[i]] = i;
+  return transpose(split, &inv);
+}
+
+// op_builder.rs:3144-3363
+Array cumsum_op(const Array& a, std::optional<size_t> axis, const Array* out) {
+  const Shape in_shape = a.shape();
+  const size_t total = shape_numel(in_shape);
+  Shape out_shape = axis ? in_shape : Shape{total};
+  Shape kshape = out_shape;
+  const int kaxis = axis ? int(*axis) : 0;
+  Dtype ct = (a.dtype == Dtype::Float32 || a.dtype == Dtype::Float64) ? a.dtype : Dtype::Int64;
+  const size_t out_size = shape_numel(out_shape);
+  check_out("cumsum", out, out_shape, ct, a, "expected", "expected");
+  StreamPtr s = pick_stream(a, out);
+  std::optional<Array> cast;
+  if (a.dtype != ct) cast = cast_array(a, ct, s);
+  const Array* aw = cast ? &*cast : &a;
+  Array r = make_output(out, out_shape, ct, a.device, s, {aw});
+  aw->data->wait_last_write_on(s);
+  std::optional<Array> flat;
+  if (!axis && !aw->layout.has_contiguous_strides()) {
+    flat = contiguous(*aw);
+    flat->data->wait_last_write_on(s);
+    aw = &*flat;
+  }
+  if (out_size > 0) {
+    Strides kstrides = axis ? aw->layout.strides : Strides{1};
+    const size_t axis_len = kshape[kaxis];
+    const size_t bpr = (axis_len + 255) / 256;
+    // capacity limit of the reference's hierarchical scan, kept for API parity (op_builder.rs:3291-3300)
+    if (bpr > 65536)
+      throw ShapeError("cumsum: axis_len " + std::to_string(axis_len) +
+                       " exceeds max supported length 16777216 (256^3)");
+    const size_t rows = out_size / std::max<size_t>(axis_len, 1);
+    const size_t scratch = bpr > 256 ? rows * (bpr + (bpr + 255) / 256) : rows * bpr;
+    BufferRef tmp;
+    if (bpr > 1) tmp = Buffer::alloc(scratch * element_size(ct), a.device, s);
+    void* tp = tmp ? tmp->ptr() : nullptr;
+    const int nd = int(kshape.size());
+    if (ct == Dtype::Int64)
+      musapy_cumsum_i64_v3((const int64_t*)aw->data_ptr(), (int64_t*)r.data_ptr(), (int64_t*)tp, nd, kshape.data(),
+                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
+    else if (ct == Dtype::Float32)
+      musapy_cumsum_f32_v3((const float*)aw->data_ptr(), (float*)r.data_ptr(), (float*)tp, nd, kshape.data(),
+                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
+    else
+      musapy_cumsum_f64_v3((const double*)aw->data_ptr(), (double*)r.data_ptr(), (double*)tp, nd, kshape.data(),
+                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
+    check_launch("cumsum");
+  }
+  aw->data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// views (rust/musapy-ops/src/indexing.rs:30-149) and materialisation (181-237)
+Array transpose(const Array& a, const std::vector<size_t>* axes) { return a.view(a.layout.transposed(axes)); }
+
+Array flip(const Array& a, size_t axis) { return a.view(a.layout.flipped(axis)); }
+
+Array slice(const Array& a, const std::vector<size_t>& start, const std::vector<size_t>& stop,
+            const std::vector<size_t>& step) {
+  return a.view(a.layout.sliced(start, stop, step));
+}
+
+Array index_select(const Array& a, size_t axis, size_t index) {
+  if (axis >= a.ndim()) throw ShapeError("index_select: axis out of bounds");
+  if (index >= a.shape()[axis]) throw ShapeError("index_select: index out of bounds");
+  Layout l;
+  l.offset = size_t(ssize_t(a.layout.offset) + ssize_t(index) * a.layout.strides[axis]);
+  for (size_t i = 0; i < a.ndim(); ++i) {
+    if (i == axis) continue;
+    l.shape.push_back(a.layout.shape[i]);
+    l.strides.push_back(a.layout.strides[i]);
+  }
+  return a.view(l);
+}
+
+Array reshape_merge_last(const Array& a, size_t k) {
+  if (k == 0 || k > a.ndim()) throw ShapeError("reshape_merge_last: invalid number of dims");
+  if (!a.layout.has_contiguous_strides()) throw ShapeError("reshape_merge_last: requires contiguous strides");
+  Shape s(a.shape().begin(), a.shape().end() - k);
+  size_t m = 1;
+  for (size_t i = a.ndim() - k; i < a.ndim(); ++i) m *= a.shape()[i];
+  s.push_back(m);
+  Layout l = Layout::from_shape(s);
+  l.offset = a.layout.offset;
+  return a.view(l);
+}
+
+Array reshape_split_last(const Array& a, size_t k) {
+  if (a.ndim() == 0 || a.shape().back() != 1) throw ShapeError("reshape_split_last: last dim must be 1");
+  Shape s(a.shape().begin(), a.shape().end() - 1);
+  for (size_t i = 0; i < k; ++i) s.push_back(1);
+  Layout l = Layout::from_shape(s);
+  l.offset = a.layout.offset;
+  return a.view(l);
+}
+
+Array contiguous(const Array& a) {
+  if (a.is_contiguous()) return a;
+  StreamPtr s = current_stream() ? current_stream() : a.stream;
+  Array r = new_array(a.shape(), a.dtype, a.device, s);
+  a.data->wait_last_write_on(s);
+  if (a.size() > 0) {
+    const size_t es = element_size(a.dtype);
+    Shape sh = a.shape();
+    Strides st = a.layout.strides;
+    const int nd = int(sh.size());
+    switch (es) {
+      case 1: musapy_copy_u8((const uint8_t*)a.data_ptr(), (uint8_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
+      case 2: musapy_copy_u16((const uint16_t*)a.data_ptr(), (uint16_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
+      case 4: musapy_copy_i32((const int32_t*)a.data_ptr(), (int32_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
+      case 8: musapy_copy_i64((const int64_t*)a.data_ptr(), (int64_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
+      default: {  // 16-byte elements: copy as pairs of 8-byte words
+        Shape sh2 = sh;
+        sh2.push_back(2);
+        Strides st2;
+        for (ssize_t x : st) st2.push_back(x * 2);
+        st2.push_back(1);
+        musapy_copy_i64((const int64_t*)a.data_ptr(), (int64_t*)r.data_ptr(), nd + 1, sh2.data(), st2.data(),
+                        s->raw());
+      }
+    }
+    check_launch("contiguous");
+  }
+  a.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+}  // namespace ops
+}  // namespace mpy

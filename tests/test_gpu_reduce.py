@@ -1,0 +1,208 @@
+"""GPU parity of reductions and cumsum against the CPU oracle.
+
+max/min/argmax/argmin and every int64 result are bit-exact (ties -> lowest index, a NaN at
+position 0 absorbs, later NaNs are skipped -- op_builder.rs:3543-3578).  Floating sums and means
+use the condition-aware bound of BASELINE.json: |gpu - cpu| <= tol * sum|x| over the reduced
+elements, tol = 1e-5 (f32) / 1e-12 (f64); the sequential CPU sum itself is that far from the
+exact sum, so an elementwise relative bound would reject every correct parallel order.
+"""
+import numpy as np
+import pytest
+
+import musapy_amd as ms
+from oracle import reference as R
+from tests.conftest import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(77)
+TOL = {np.float32: 1e-5, np.float64: 1e-12, np.complex64: 1e-5, np.complex128: 1e-12}
+
+
+def dev(x):
+    return ms.from_numpy(np.ascontiguousarray(x))
+
+
+def abs_sum(x, axis, keepdims):
+    ax = axis if axis is None or isinstance(axis, tuple) else (axis,)
+    return np.sum(np.abs(x.astype(np.complex128 if np.iscomplexobj(x) else np.float64)), axis=ax, keepdims=keepdims)
+
+
+def check_reduce(kind, x, axis=None, keepdims=False, gpu_x=None):
+    gx = dev(x) if gpu_x is None else gpu_x
+    got = getattr(ms, kind)(gx, axis=axis, keepdims=keepdims).numpy()
+    want = R.reduce(x, kind, axis, keepdims)
+    what = f"{kind} {x.dtype} {x.shape} axis={axis} keepdims={keepdims}"
+    if kind in ("max", "min", "argmax", "argmin") or want.dtype == np.int64:
+        assert_bits_equal(got, want, what)
+        return
+    assert got.shape == want.shape and got.dtype == want.dtype, what
+    tol = TOL[want.dtype.type]
+    if kind == "prod":
+        # products have no bound in BASELINE.json; compare relatively, allowing sqrt(n) roundings
+        n = x.size // max(want.size, 1)
+        eps = 1.2e-7 if want.dtype in (np.float32, np.complex64) else 2.3e-16
+        err = np.abs(got.astype(np.complex128) - want) / np.maximum(np.abs(want), 1e-300)
+        assert np.all(err <= 20 * eps * np.sqrt(n) + 4 * eps), f"{what}: max rel err {err.max()}"
+        return
+    scale = abs_sum(x, axis, keepdims)
+    if kind == "mean":
+        n = x.size // max(want.size, 1)
+        scale = scale / max(n, 1)
+    err = np.abs(got.astype(np.complex128) - want.astype(np.complex128))
+    assert np.all(err <= tol * scale + 1e-30), f"{what}: max err {err.max()} vs bound {tol * scale.max()}"
+
+
+SHAPES_AXES = [
+    ((257,), [None, 0]),
+    ((4, 1000), [0, 1, None, -1]),
+    ((1000, 4), [0, 1]),
+    ((33, 65, 7), [0, 1, 2, None]),
+    ((5000, 3), [0, 1]),
+    ((3, 1, 4096), [2, 1, 0]),
+    ((2, 300000), [1]),
+]
+
+
+@pytest.mark.parametrize("kind", ["sum", "prod", "max", "min", "mean", "argmax", "argmin"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_reduce_shapes(kind, dt):
+    for shape, axes in SHAPES_AXES:
+        if dt == np.int64:
+            x = RNG.integers(-1000, 1000, shape).astype(np.int64)
+        elif kind == "prod":
+            x = RNG.uniform(0.9, 1.1, shape).astype(dt)
+        else:
+            x = RNG.standard_normal(shape).astype(dt)
+        for ax in axes:
+            check_reduce(kind, x, ax)
+        check_reduce(kind, x, axes[0], keepdims=True)
+
+
+@pytest.mark.parametrize("kind", ["max", "min", "argmax", "argmin"])
+def test_ordered_semantics_planted(kind):
+    # ties, +-0 and NaN at k=0 / later, spread over tiles of the parallel paths
+    for shape, axis in (((64, 3000), 1), ((3000, 64), 0), ((1, 1 << 20), 1), ((16, 37), 1)):
+        x = RNG.integers(-2, 3, shape).astype(np.float32)
+        flat_axis_len = shape[axis]
+        idx = [slice(None)] * 2
+        idx[axis] = 0
+        x[tuple(idx)][::5] = np.nan           # NaN at k = 0 in every 5th output
+        idx[axis] = flat_axis_len // 2
+        x[tuple(idx)][1::3] = np.nan          # a later NaN
+        x[tuple(idx)][2::7] = -0.0
+        check_reduce(kind, x, axis)
+        check_reduce(kind, x.astype(np.float64), axis)
+    z = np.zeros((8, 5000), np.float32)
+    z[:, ::2] = -0.0
+    check_reduce(kind, z, 1)
+    check_reduce(kind, z.T.copy(), 0)
+
+
+@pytest.mark.parametrize("kind", ["sum", "max", "argmax", "mean"])
+def test_reduce_views(kind):
+    base = RNG.standard_normal((64, 96)).astype(np.float32)
+    B = dev(base)
+    for nv, dv in ((lambda x: x[:, ::-1], lambda a: ms.flip(a, 1)),
+                   (lambda x: x.T, lambda a: ms.transpose(a)),
+                   (lambda x: x[3:60:2, 5:90], lambda a: ms.slice(a, [(3, 60, 2), (5, 90, 1)]))):
+        for ax in (0, 1, None):
+            check_reduce(kind, np.ascontiguousarray(nv(base)), ax, gpu_x=dv(B))
+
+
+@pytest.mark.parametrize("kind", ["sum", "mean", "prod", "max", "min", "argmax", "argmin"])
+def test_multi_axis(kind):
+    x = RNG.standard_normal((6, 7, 8)).astype(np.float32)
+    if kind == "prod":
+        x = RNG.uniform(0.9, 1.1, (6, 7, 8)).astype(np.float32)
+    for axes in ((0, 1), (1, 2), (0, 2), (0, 1, 2), (-1, 0)):
+        for keep in (False, True):
+            check_reduce(kind, x, axes, keep)
+
+
+@pytest.mark.parametrize("dt", [np.complex64, np.complex128])
+def test_complex_reductions(dt):
+    for shape, axes in (((3, 4), [None, 0, 1, (0, 1), -1]), ((16, 64, 64), [(1, 2), 0, 2]), ((4, 200000), [1])):
+        z = (RNG.standard_normal(shape) + 1j * RNG.standard_normal(shape)).astype(dt)
+        for ax in axes:
+            check_reduce("sum", z, ax)
+            check_reduce("mean", z, ax)
+        zp = (np.exp(1j * RNG.uniform(-0.1, 0.1, shape[-1:]))).astype(dt)
+        check_reduce("prod", zp, None)
+    with pytest.raises(ms.DtypeError):
+        ms.max(dev(np.array([1 + 2j], np.complex128)))
+
+
+def test_reduce_errors_and_edges():
+    x = dev(np.ones((2, 3), np.float32))
+    with pytest.raises(ms.ShapeError):
+        ms.sum(x, axis=5)
+    with pytest.raises(ms.ShapeError):
+        ms.sum(x, axis=(0, 0))
+    with pytest.raises(ms.ShapeError):
+        ms.sum(x, axis=(0, 1), out=dev(np.zeros(2, np.float32)))
+    with pytest.raises(Exception):
+        ms.sum(x, axis=0, out=dev(np.zeros(2, np.int64)))
+    r = ms.sum(dev(np.array([5.0], np.float32)))
+    assert r.shape == () and r.item() == 5.0
+    assert ms.sum(dev(np.array([1, 2, 3], np.int8))).dtype == "i64"
+    e = ms.sum(dev(np.zeros((3, 0), np.float32)), axis=1)
+    assert e.numpy().tolist() == [0.0, 0.0, 0.0]
+    with pytest.raises(ms.ShapeError):
+        ms.max(dev(np.zeros((3, 0), np.float32)), axis=1)
+    out = dev(np.zeros(3, np.float32))
+    ms.sum(dev(np.ones((3, 4), np.float32)), axis=1, out=out)
+    assert out.tolist() == [4.0, 4.0, 4.0]
+
+
+# ---------------------------------------------------------------------------------------------
+# cumsum
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_cumsum_shapes(dt):
+    cases = [((1300,), 0), ((1537,), 0), ((3, 70000), 1), ((65536,), 0), ((65537,), 0), ((5, 7), 1),
+             ((64, 4097), 1), ((2000, 3), 0), ((7, 300, 5), 1), ((4, 12288), 1)]
+    for shape, ax in cases:
+        x = RNG.integers(-50, 50, shape).astype(dt) if dt == np.int64 else RNG.random(shape).astype(dt)
+        got = ms.cumsum(dev(x), axis=ax).numpy()
+        want = R.cumsum(x, ax)
+        if dt == np.int64:
+            assert_bits_equal(got, want, f"cumsum {shape}")
+        else:
+            scale = np.cumsum(np.abs(x.astype(np.float64)), axis=ax)
+            assert np.all(np.abs(got - want) <= TOL[dt] * scale), f"cumsum {dt} {shape} axis {ax}"
+
+
+def test_cumsum_reference_cases():
+    # tests/python/test_reduction.py:337-423 (cumsum of ones, capacity limit)
+    for n in (65536, 65537, 1_000_000):
+        r = ms.cumsum(ms.ones(n, dtype="i64"), axis=0)
+        assert ms.sum(r).item() == n * (n + 1) // 2
+        v = r.numpy()
+        assert v[-1] == n and v[min(65535, n - 1)] == min(65536, n)
+    x = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    assert ms.cumsum(dev(x)).tolist() == [1.0, 3.0, 6.0, 10.0]
+    assert ms.cumsum(dev(x), axis=0).tolist() == [[1.0, 2.0], [4.0, 6.0]]
+    assert ms.cumsum(dev(np.array([1, 2, 3], np.int64)), axis=0).dtype == "i64"
+    with pytest.raises(ms.ShapeError):
+        ms.cumsum(ms.ones(256**3 + 1, dtype="f32"), axis=0)
+
+
+def test_cumsum_views_and_exact_orders():
+    base = RNG.random((300, 200)).astype(np.float64)
+    B = dev(base)
+    # column and strided scans add in the CPU's order: bit-exact
+    assert_bits_equal(ms.cumsum(B, axis=0).numpy(), R.cumsum(base, 0), "column scan")
+    assert_bits_equal(ms.cumsum(ms.transpose(B), axis=1).numpy(), R.cumsum(base.T, 1), "transposed scan")
+    flat = ms.cumsum(ms.transpose(B)).numpy()
+    want = R.cumsum(base.T, None)
+    assert np.all(np.abs(flat - want) <= 1e-12 * np.cumsum(np.abs(base.T.reshape(-1))))
+
+
+def test_cumsum_deterministic():
+    x = RNG.random((8, 1 << 18)).astype(np.float32)
+    X = dev(x)
+    a = ms.cumsum(X, axis=1).numpy()
+    for _ in range(3):
+        assert_bits_equal(ms.cumsum(X, axis=1).numpy(), a, "cumsum run-to-run")
+    s = ms.sum(X, axis=1).numpy()
+    for _ in range(3):
+        assert_bits_equal(ms.sum(X, axis=1).numpy(), s, "sum run-to-run")
