@@ -6,10 +6,10 @@ that metric names:
     C1  add      f32, 16,777,216 elements U(-1,1), seed 0            12 B/elem
     C4  sum      axis=-1 of an (8192, 8192) f32 N(0,1) array, seed 0   4 B/elem + 4 B/row
     C4  argmax   axis=1 of the same array -> int64                    4 B/elem + 8 B/row
-Inputs are resident in HBM before timing.  Each launch is bracketed by HIP events on the
-stream it runs on, and a 1 GiB write is issued before every launch (outside the events) so the
-256 MB Infinity Cache cannot serve the inputs.  `value` = algorithmic bytes of the step /
-summed kernel time.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
+Inputs are resident in HBM before timing.  Each op is launched K times back-to-back between two
+HIP events on the stream it runs on, with outputs preallocated (out=) and the inputs rotated
+over 4 device copies, so every launch streams its inputs from HBM rather than from the 256 MB
+Infinity Cache.  `value` = algorithmic bytes of the step / summed average launch time.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
 musapy's CPU path) on the same step.
 
     python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
@@ -34,91 +34,96 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--all", action="store_true", help="also time every BASELINE config (table on stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--no-flush", action="store_true", help="do not evict the Infinity Cache between launches")
     return p.parse_args()
 
 
-class Bench:
-    def __init__(self, ms, flush=True):
+COPIES = 4  # input copies rotated between launches (4 x the working set >> the 256 MB MALL)
+
+
+class Timer:
+    """HIP events on device 0's stream (the stream every op below is launched on)."""
+
+    def __init__(self, ms):
         self.ms = ms
-        self.flush_buf = ms.from_numpy(np.zeros(1 << 28, np.float32)) if flush else None  # 1 GiB
-        self.timer = ms._core._Timer(0)
+        self.t = ms._core._Timer(0)
 
-    def flush(self):
-        if self.flush_buf is not None:
-            self.ms._core._fill_u32(self.flush_buf, 0x3F800000)
+    def run(self, launches):
+        """Launches back-to-back between two events; returns the average launch time (ms)."""
+        self.t.start()
+        for f in launches:
+            f()
+        self.t.stop()
+        return self.t.elapsed_ms() / len(launches)
 
-    def time_op(self, fn, reps):
-        """Average kernel time (ms) of fn() over reps launches, each after a cache flush."""
-        total = 0.0
-        out = None
-        for _ in range(reps):
-            self.flush()
-            self.timer.start()
-            out = fn()
-            self.timer.stop()
-            total += self.timer.elapsed_ms()
-        return total / reps, out
+
+def _copies(ms, host, n=COPIES):
+    return [ms.from_numpy(host) for _ in range(n)]
 
 
 def step_ops(ms):
+    """The three ops of one step, each as a function of the launch index (inputs rotate)."""
     rng = np.random.default_rng(0)
     a = rng.uniform(-1, 1, 16_777_216).astype(np.float32)
     b = rng.uniform(-1, 1, 16_777_216).astype(np.float32)
     x = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
-    A, B, X = ms.from_numpy(a), ms.from_numpy(b), ms.from_numpy(x)
+    A, B, X = _copies(ms, a), _copies(ms, b), _copies(ms, x)
+    C = ms.from_numpy(np.zeros_like(a))
+    S = ms.from_numpy(np.zeros(8192, np.float32))
+    I = ms.from_numpy(np.zeros(8192, np.int64))
     n = 8192 * 8192
     ops = [
-        ("C1 add f32 16,777,216", lambda: ms.add(A, B), 12 * 16_777_216),
-        ("C4 sum axis=-1 (8192,8192) f32", lambda: ms.sum(X, axis=-1), 4 * n + 4 * 8192),
-        ("C4 argmax axis=1 (8192,8192) f32", lambda: ms.argmax(X, axis=1), 4 * n + 8 * 8192),
+        ("C1 add f32 16,777,216", lambda i: ms.add(A[i % COPIES], B[i % COPIES], out=C), 12 * 16_777_216),
+        ("C4 sum axis=-1 (8192,8192) f32", lambda i: ms.sum(X[i % COPIES], axis=-1, out=S), 4 * n + 4 * 8192),
+        ("C4 argmax axis=1 (8192,8192) f32", lambda i: ms.argmax(X[i % COPIES], axis=1, out=I), 4 * n + 8 * 8192),
     ]
     host = {"a": a, "b": b, "x": x}
     return ops, host
 
 
 def all_config_ops(ms):
-    """Every BASELINE config op (for the per-config table)."""
+    """Every BASELINE config op (for the per-config table); inputs rotate over 3 copies."""
+    K = 3
     rng = np.random.default_rng(0)
     ops = []
     a64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
     b64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
-    A64, B64 = ms.from_numpy(a64), ms.from_numpy(b64)
-    ops.append(("C1-64M add f32 67,108,864", lambda: ms.add(A64, B64), 12 * 67_108_864))
-    ops.append(("full sum f32 64M", lambda: ms.sum(A64), 4 * 67_108_864 + 4))
-    ops.append(("full argmax f32 64M", lambda: ms.argmax(A64), 4 * 67_108_864 + 8))
+    A64, B64 = _copies(ms, a64, K), _copies(ms, b64, K)
+    ops.append(("C1-64M add f32 67,108,864", lambda i: ms.add(A64[i % K], B64[i % K]), 12 * 67_108_864))
+    ops.append(("full sum f32 64M", lambda i: ms.sum(A64[i % K]), 4 * 67_108_864 + 4))
+    ops.append(("full argmax f32 64M", lambda i: ms.argmax(A64[i % K]), 4 * 67_108_864 + 8))
     r = np.random.default_rng(0)
-    ca = ms.from_numpy(r.uniform(-1, 1, (4096, 1)).astype(np.float32))
-    cb = ms.from_numpy(r.uniform(-1, 1, (8192,)).astype(np.float32))
-    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda: ms.add(ca, cb), 4 * 33_554_432 + 4 * 4096 + 4 * 8192))
-    xt = ms.transpose(ms.from_numpy(np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32)))
-    ops.append(("C2 exp transposed (8192,4096)^T", lambda: ms.exp(xt), 8 * 33_554_432))
+    ca, cb = r.uniform(-1, 1, (4096, 1)).astype(np.float32), r.uniform(-1, 1, (8192,)).astype(np.float32)
+    CA, CB = _copies(ms, ca, K), _copies(ms, cb, K)
+    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda i: ms.add(CA[i % K], CB[i % K]),
+                4 * 33_554_432 + 4 * 4096 + 4 * 8192))
+    xt = [ms.transpose(c) for c in _copies(ms, np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32), K)]
+    ops.append(("C2 exp transposed (8192,4096)^T", lambda i: ms.exp(xt[i % K]), 8 * 33_554_432))
     r = np.random.default_rng(0)
-    i64 = ms.from_numpy(r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64))
-    f64 = ms.from_numpy(r.standard_normal((2048, 2048, 4)))
+    i64 = _copies(ms, r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64), K)
+    f64 = _copies(ms, r.standard_normal((2048, 2048, 4)), K)
     N = 16_777_216
-    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda: ms.add(i64, f64), 24 * N))
-    s = ms.add(i64, f64)
-    ops.append(("C3 clamp f64", lambda: ms.clamp(s, -1.0, 1.0), 16 * N))
-    c = ms.clamp(s, -1.0, 1.0)
-    ops.append(("C3 astype f64->f32", lambda: ms.astype(c, "f32"), 12 * N))
-    f = ms.astype(c, "f32")
-    ops.append(("C3 astype f32->bf16", lambda: ms.astype(f, "bf16"), 6 * N))
-    ops.append(("C3 astype f32->f16", lambda: ms.astype(f, "f16"), 6 * N))
-    X = ms.from_numpy(np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32))
+    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda i: ms.add(i64[i % K], f64[i % K]), 24 * N))
+    s = [ms.add(i64[k], f64[k]) for k in range(K)]
+    ops.append(("C3 clamp f64", lambda i: ms.clamp(s[i % K], -1.0, 1.0), 16 * N))
+    c = [ms.clamp(s[k], -1.0, 1.0) for k in range(K)]
+    ops.append(("C3 astype f64->f32", lambda i: ms.astype(c[i % K], "f32"), 12 * N))
+    f = [ms.astype(c[k], "f32") for k in range(K)]
+    ops.append(("C3 astype f32->bf16", lambda i: ms.astype(f[i % K], "bf16"), 6 * N))
+    ops.append(("C3 astype f32->f16", lambda i: ms.astype(f[i % K], "f16"), 6 * N))
+    X = _copies(ms, np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32), K)
     n = 8192 * 8192
-    ops.append(("C4 sum axis=0", lambda: ms.sum(X, axis=0), 4 * n + 4 * 8192))
-    ops.append(("C4 mean axis=-1", lambda: ms.mean(X, axis=-1), 4 * n + 4 * 8192))
-    ops.append(("C4 mean axis=0", lambda: ms.mean(X, axis=0), 4 * n + 4 * 8192))
-    ops.append(("C4 max axis=(0,1)", lambda: ms.max(X, axis=(0, 1)), 4 * n + 4))
-    ops.append(("C4 argmin axis=1", lambda: ms.argmin(X, axis=1), 4 * n + 8 * 8192))
-    y = ms.from_numpy(np.random.default_rng(0).random((1024, 65536)))
-    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda: ms.cumsum(y, axis=1), 16 * 1024 * 65536))
+    ops.append(("C4 sum axis=0", lambda i: ms.sum(X[i % K], axis=0), 4 * n + 4 * 8192))
+    ops.append(("C4 mean axis=-1", lambda i: ms.mean(X[i % K], axis=-1), 4 * n + 4 * 8192))
+    ops.append(("C4 mean axis=0", lambda i: ms.mean(X[i % K], axis=0), 4 * n + 4 * 8192))
+    ops.append(("C4 max axis=(0,1)", lambda i: ms.max(X[i % K], axis=(0, 1)), 4 * n + 4))
+    ops.append(("C4 argmin axis=1", lambda i: ms.argmin(X[i % K], axis=1), 4 * n + 8 * 8192))
+    y = _copies(ms, np.random.default_rng(0).random((1024, 65536)), K)
+    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda i: ms.cumsum(y[i % K], axis=1), 16 * 1024 * 65536))
     r = np.random.default_rng(0)
     z = (r.standard_normal((16, 1024, 1024), dtype=np.float32)
          + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
-    Z = ms.from_numpy(z)
-    ops.append(("C5 c64 sum axis=(1,2)", lambda: ms.sum(Z, axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128))
+    Z = _copies(ms, z, K)
+    ops.append(("C5 c64 sum axis=(1,2)", lambda i: ms.sum(Z[i % K], axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128))
     return ops
 
 
@@ -150,25 +155,25 @@ def main():
         sys.exit(2)
     import musapy_amd as ms
 
-    b = Bench(ms, flush=not args.no_flush)
+    timer = Timer(ms)
     ops, host = step_ops(ms)
-    for name, fn, _ in ops:  # warm-up (first launch loads code objects)
-        for _ in range(max(args.warmup, 1)):
-            fn()
+    for name, fn, _ in ops:  # warm-up (first launches load code objects, fill the memory pool)
+        for i in range(max(args.warmup, 1)):
+            fn(i)
     ms.synchronize()
     per_op = {}
     t0 = time.perf_counter()
     ms.synchronize()
-    for _ in range(args.steps):
-        for name, fn, bytes_ in ops:
-            t, _ = b.time_op(fn, 1)
-            per_op.setdefault(name, []).append(t)
+    # K steps: each op is launched K times back-to-back between two events (inputs rotate over
+    # COPIES device copies, so every launch streams from HBM)
+    for name, fn, _ in ops:
+        per_op[name] = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(args.steps)])
     ms.synchronize()
     wall = time.perf_counter() - t0
     table = {}
     total_bytes, total_ms = 0, 0.0
     for name, fn, bytes_ in ops:
-        t = float(np.mean(per_op[name]))
+        t = float(per_op[name])
         table[name] = {"ms": round(t, 5), "algo_bytes": bytes_, "GBps": round(bytes_ / t / 1e6, 1),
                        "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4)}
         total_bytes += bytes_
@@ -184,6 +189,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(total_ms, 5),
         "wall_ms_per_step": round(wall * 1e3 / args.steps, 3),
+        "timing": f"HIP events around {args.steps} back-to-back launches per op, inputs rotated over {COPIES} copies",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -203,8 +209,9 @@ def main():
     if args.all:
         rows = []
         for name, fn, bytes_ in all_config_ops(ms):
-            fn()
-            t, _ = b.time_op(fn, 5)
+            fn(0)
+            ms.synchronize()
+            t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(6)])
             rows.append({"op": name, "ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
                          "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4)})
             print(json.dumps(rows[-1]), file=sys.stderr, flush=True)

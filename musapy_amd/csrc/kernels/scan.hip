@@ -35,20 +35,35 @@ template <> __device__ inline double from_bits<double>(uint64_t b) { return __lo
 template <> __device__ inline float from_bits<float>(uint64_t b) { return __uint_as_float(uint32_t(b)); }
 template <> __device__ inline uint64_t from_bits<uint64_t>(uint64_t b) { return b; }
 
-// status words per (row, tile): [flag, aggregate bits, inclusive bits]; word 0 is the counter
-enum : uint64_t { kFlagNone = 0, kFlagAgg = 1, kFlagIncl = 2 };
-
-__device__ inline uint64_t ld_acquire(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Published look-back values.  Agent-scope acquire/release would make every publish write back
+// and every poll invalidate a whole L2 on this multi-XCD part, so there are no fences at all:
+// a value is stored as W 64-bit words, each holding a 32-bit slice of its bits next to a
+// "published" tag, with relaxed (but coherent) 64-bit atomics.  Each word is written once per
+// launch, so a reader that sees the tag on every word holds the final value.
 __device__ inline uint64_t ld_relaxed(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ inline void st_relaxed(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline void st_release(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+constexpr uint64_t kTag = uint64_t(1) << 32;
+
+template <int W>
+__device__ inline void publish_value(uint64_t* w, uint64_t bits) {
+  st_relaxed(w, kTag | (bits & 0xffffffffu));
+  if (W == 2) st_relaxed(w + 1, kTag | (bits >> 32));
+}
+template <int W>
+__device__ inline bool read_value(const uint64_t* w, uint64_t& bits) {
+  uint64_t lo = ld_relaxed(w);
+  if (!(lo & kTag)) return false;
+  uint64_t hi = 0;
+  if (W == 2) {
+    hi = ld_relaxed(w + 1);
+    if (!(hi & kTag)) return false;
+  }
+  bits = (lo & 0xffffffffu) | ((hi & 0xffffffffu) << 32);
+  return true;
 }
 
 __global__ void k_scan_clear(uint64_t* w, uint64_t n) {
@@ -62,7 +77,7 @@ struct RowScanArgs {
   uint32_t rows;
   uint32_t tiles;       // tiles per row
   uint32_t* counter;    // tile claim counter; nullptr when tiles == 1 (no look-back)
-  uint64_t* status;     // [rows * tiles][3]: flag, aggregate bits, inclusive bits
+  uint64_t* status;     // per row: inclusive prefixes of tiles 0..T-2, aggregates of 1..T-2
   uint32_t* err;        // set when a look-back wait exceeds its bound
   uint32_t spin_limit;
   bool vec;             // 16-byte aligned rows
@@ -144,30 +159,31 @@ __global__ __launch_bounds__(kSBlock) void k_scan_rows(const T* __restrict__ a, 
   // the exclusive prefix inside the tile: wave offset + lane offset (fixed association)
   A local = wave_off + lane_excl;
 
-  // tile prefix from the look-back
+  // tile prefix from the look-back (one lane; the rest of the block waits at the barrier)
   if (tid == 0) {
     A P = A(0);
     if (sa.counter) {
-      uint64_t* st = sa.status + uint64_t(3) * (uint64_t(row) * sa.tiles + chunk);
+      constexpr int W = sizeof(A) == 4 ? 1 : 2;
+      const uint32_t NT = sa.tiles;  // >= 2 here; the last tile publishes nothing
+      uint64_t* rowp = sa.status + uint64_t(row) * (2 * NT - 3) * W;
+      auto incl_of = [&](uint32_t c) { return rowp + uint64_t(c) * W; };            // tiles 0..T-2
+      auto agg_of = [&](uint32_t c) { return rowp + uint64_t(NT - 1 + c - 1) * W; };  // tiles 1..T-2
       if (chunk == 0) {
-        st_relaxed(st + 2, bits_of(agg));
-        st_release(st, kFlagIncl);
+        publish_value<W>(incl_of(0), bits_of(agg));
       } else {
-        st_relaxed(st + 1, bits_of(agg));
-        st_release(st, kFlagAgg);
-        // walk back to the nearest tile with a published inclusive prefix
+        if (chunk <= NT - 2) publish_value<W>(agg_of(chunk), bits_of(agg));
+        // walk back to the nearest tile whose inclusive prefix is published
         uint32_t j = chunk - 1;
         uint32_t spins = 0;
         bool ok = true;
+        uint64_t b = 0;
         for (;;) {
-          const uint64_t* sj = sa.status + uint64_t(3) * (uint64_t(row) * sa.tiles + j);
-          uint64_t f = ld_acquire(sj);
-          if (f == kFlagIncl) {
-            P = from_bits<A>(ld_relaxed(sj + 2));
+          if (read_value<W>(incl_of(j), b)) {
+            P = from_bits<A>(b);
             break;
           }
-          if (f == kFlagAgg) {
-            --j;  // chunk 0 always publishes an inclusive prefix, so j stays >= 0
+          if (j > 0 && read_value<W>(agg_of(j), b)) {  // tile 0 only ever publishes an inclusive prefix
+            --j;
             continue;
           }
           if (++spins > sa.spin_limit) {
@@ -181,12 +197,11 @@ __global__ __launch_bounds__(kSBlock) void k_scan_rows(const T* __restrict__ a, 
         } else {
           // re-fold the aggregates after j in order: P(m) = P(m-1) + A(m)
           for (uint32_t m = j + 1; m < chunk; ++m) {
-            const uint64_t* sm = sa.status + uint64_t(3) * (uint64_t(row) * sa.tiles + m);
-            P = P + from_bits<A>(ld_relaxed(sm + 1));
+            read_value<W>(agg_of(m), b);  // seen published during the walk back
+            P = P + from_bits<A>(b);
           }
         }
-        st_relaxed(st + 2, bits_of(P + agg));
-        st_release(st, kFlagIncl);
+        if (chunk <= NT - 2) publish_value<W>(incl_of(chunk), bits_of(P + agg));
       }
     }
     s_prefix = P;
@@ -277,12 +292,14 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
       // tmp capacity per the caller's formula: rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
       uint64_t bpr = (p.L + 255) / 256;
       uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
-      uint64_t words = 2 + uint64_t(3) * p.rows * sa.tiles;  // counter + error word + status
+      // word 0: claim counter; then per row (2*tiles-3)*W status words (inclusive prefixes of
+      // tiles 0..T-2, aggregates of tiles 1..T-2); last word: error flag
+      const uint64_t W = sizeof(T) == 4 ? 1 : 2;
+      uint64_t words = 2 + uint64_t(p.rows) * (2 * uint64_t(sa.tiles) - 3) * W;
       if (tmp == nullptr || words * 8 > cap) {
         g_scan_error = 1;
         return;
       }
-      // word 0: claim counter, words 1..3*rows*tiles: status triples, last word: error flag
       uint64_t* w = reinterpret_cast<uint64_t*>(tmp);
       sa.counter = reinterpret_cast<uint32_t*>(w);
       sa.status = w + 1;

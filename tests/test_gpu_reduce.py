@@ -70,7 +70,9 @@ def test_reduce_shapes(kind, dt):
         if dt == np.int64:
             x = RNG.integers(-1000, 1000, shape).astype(np.int64)
         elif kind == "prod":
-            x = RNG.uniform(0.9, 1.1, shape).astype(dt)
+            # keep the product O(1): a product that underflows compares the CPU's stuck denormal
+            # with a tree's exact zero, which says nothing about either
+            x = RNG.uniform(0.999, 1.001, shape).astype(dt)
         else:
             x = RNG.standard_normal(shape).astype(dt)
         for ax in axes:
