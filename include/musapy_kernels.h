@@ -248,9 +248,24 @@ void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t*
 void musapy_copy_u8(const uint8_t* input, uint8_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
 void musapy_copy_u16(const uint16_t* input, uint16_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
 
+/* ---- fused mixed-dtype binary (new; no counterpart in kernels.rs) ----
+ * c = op(C(a), C(b)) where C(x) is the Rust `as` cast to c_dtype used by the cast kernels above:
+ * bit-identical to musapy's cast-then-compute promotion path (op_builder.rs:410-417, 1055-1119)
+ * in one pass instead of two.  Supported (a, b) -> c triples: one of a/b already has dtype c,
+ * the other is int32/int64/float32/float64, c is float32/float64.  Returns 0 when launched,
+ * -1 when the triple is not supported (nothing is launched; use the cast + binary symbols). */
+enum {
+  MUSAPY_DT_BOOL = 0, MUSAPY_DT_I8, MUSAPY_DT_I16, MUSAPY_DT_I32, MUSAPY_DT_I64, MUSAPY_DT_U8, MUSAPY_DT_U16,
+  MUSAPY_DT_U32, MUSAPY_DT_U64, MUSAPY_DT_F16, MUSAPY_DT_F32, MUSAPY_DT_F64, MUSAPY_DT_BF16, MUSAPY_DT_C64,
+  MUSAPY_DT_C128
+};
+enum { MUSAPY_OP_ADD = 0, MUSAPY_OP_SUB, MUSAPY_OP_MUL, MUSAPY_OP_DIV, MUSAPY_OP_POW };
+int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, int b_dtype, void* c, int c_dtype, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+
 /* ---- wrapper-level error (new; no counterpart in kernels.rs) ----
  * Returns and clears the calling thread's last wrapper error: 0 none, 1 a cumsum scratch buffer
- * that is NULL or smaller than the reference's scratch formula requires. */
+ * that is NULL or smaller than the reference's scratch formula requires, 2 a reduction whose
+ * per-tile length reaches 2^31 elements (pass more tiles). */
 int musapy_kernels_take_error(void);
 
 /* ---- planning helper (new; no counterpart in kernels.rs) ----

@@ -4,14 +4,16 @@
 // vec4 / scalar kernels (elementwise.mu:35-208, 295-394, 451-536).  Instead of one thread per
 // element decoding every dimension with 64-bit div/mod, the wrapper coalesces dimensions on the
 // host (plan.hpp) and picks one of four variants:
-//   flat       every operand contiguous or a broadcast scalar: 16-byte vector loads/stores,
-//              UNROLL independent vectors in flight per thread;
+//   flat       every operand contiguous or a broadcast scalar: one 16-byte vector per operand
+//              per lane, many short blocks;
+//   tiles      (binary, long rows) column tiles that walk down the rows: an operand broadcast
+//              along the rows stays in registers, a per-row scalar costs one load per row;
 //   rows       output rows of the innermost dim; the outer coordinates of a row are decoded
 //              once with 32-bit magic division, the inner dim is streamed per operand as
 //              vector (stride 1), broadcast (stride 0) or gather (any other stride);
 //   transpose  single-input ops whose input is unit-stride along some other dim (a transposed
-//              or permuted view): 64x64 tiles staged through LDS so both the read and the write
-//              are coalesced;
+//              or permuted view): 64 x (32*VEC) tiles staged through LDS so that both the read
+//              and the write are 16-byte coalesced accesses;
 //   generic    64-bit per-element decode, only for shapes beyond the 32-bit limits above.
 #include "kcommon.hpp"
 #include "ew_ops.hpp"
@@ -186,48 +188,166 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
 }
 
 // ---------------------------------------------------------------------------------------------
+// mixed dtypes: c = f(TC(a), TC(b)) with the cast functors of the cast kernels, i.e. exactly the
+// reference's cast-then-compute (op_builder.rs:410-417) without materialising the cast.
+template <int VEC, class F, class TC, class TA, class TB>
+__global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restrict__ a, const TB* __restrict__ b,
+                                                              TC* __restrict__ c, uint64_t n, F f) {
+  const uint64_t i0 = (uint64_t(blockIdx.x) * kBlock + threadIdx.x) * VEC;
+  const CastF<TA, TC> ca{};
+  const CastF<TB, TC> cb{};
+  if (i0 + VEC <= n) {
+    Vec<TA, VEC> x = vload<TA, VEC>(a + i0);
+    Vec<TB, VEC> y = vload<TB, VEC>(b + i0);
+    Vec<TC, VEC> z;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) z.v[k] = f(ca(x.v[k]), cb(y.v[k]));
+    vstore<TC, VEC>(c + i0, z);
+  } else {
+    for (uint64_t i = i0; i < n; ++i) c[i] = f(ca(a[i]), cb(b[i]));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// tiles: the broadcast form of rows.  A block owns kBlock*VEC columns of the innermost dim and a
+// run of RB rows; each lane walks its VEC columns down the rows.  An operand whose outer strides
+// are all zero (a row vector broadcast over rows) is loaded once into registers; an operand with
+// inner stride zero (a column broadcast along the row) costs one load per row.
+struct TileArgs {
+  RowIndexer<3> ix;   // outer dims: [0] out, [1] a, [2] b strides
+  uint32_t L, rows, rb;
+  bool aligned;
+  bool a_inv, b_inv;  // operand does not depend on the row
+};
+
+template <int VEC, class F, class T>
+__global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In<T> b, int64_t sb, T* __restrict__ c,
+                                                         TileArgs ta, F f) {
+  const uint32_t col = (blockIdx.x * kBlock + threadIdx.x) * VEC;
+  if (col >= ta.L) return;
+  const bool full = ta.aligned || col + VEC <= ta.L;
+  const bool vec = full && ta.aligned;
+  const uint32_t r0 = blockIdx.y * ta.rb;
+  const uint32_t r1 = r0 + ta.rb < ta.rows ? r0 + ta.rb : ta.rows;
+  T ia[VEC], ib[VEC];  // row-invariant operands
+  if (ta.a_inv) load_item<VEC, T>(a.p, a.mode, sa, col, ta.L, vec, ia);
+  if (ta.b_inv) load_item<VEC, T>(b.p, b.mode, sb, col, ta.L, vec, ib);
+  constexpr int RU = 4;  // rows whose loads are issued before their stores
+  for (uint32_t r = r0; r < r1; r += RU) {
+    T xa[RU][VEC], xb[RU][VEC];
+    int64_t oc[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      if (r + u >= r1) break;
+      int64_t off[3];
+      row_offsets<3>(ta.ix, r + u, off);
+      oc[u] = off[0];
+      if (ta.a_inv) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) xa[u][k] = ia[k];
+      } else {
+        load_item<VEC, T>(a.p + off[1], a.mode, sa, col, ta.L, vec, xa[u]);
+      }
+      if (ta.b_inv) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) xb[u][k] = ib[k];
+      } else {
+        load_item<VEC, T>(b.p + off[2], b.mode, sb, col, ta.L, vec, xb[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      if (r + u >= r1) break;
+      T* cp = c + oc[u] + col;
+      if (vec) {
+        Vec<T, VEC> v;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) v.v[k] = f(xa[u][k], xb[u][k]);
+        vstore<T, VEC>(cp, v);
+      } else {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+          if (col + k < ta.L) cp[k] = f(xa[u][k], xb[u][k]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // transpose: single input that is unit-stride along dim P while the output is unit-stride along
 // the innermost dim L.  A block moves a kTP x kTL tile through LDS.  Remaining dims are batch.
-constexpr int kTP = 64, kTL = 64;
-
 struct TransposeArgs {
   uint64_t P, L;           // extents of the two tiled dims
   int64_t in_sL;           // input stride along L (input stride along P is 1)
   int64_t out_sP;          // output stride along P (output stride along L is 1)
   FastDiv tilesL, tilesP;  // tile counts
   RowIndexer<2> batch;     // batch dims: [0] output strides, [1] input strides
+  bool vec_in, vec_out;    // 16-byte aligned vector access possible on each side
 };
+
+// Tile geometry: TL = 64 along L (output-contiguous), TP = 32 lanes x VI elements along P
+// (input-contiguous); every global access is a 16-byte vector when alignment allows.
+template <class TI> constexpr int tr_vin() { return sizeof(TI) >= 8 ? 2 : (sizeof(TI) == 4 ? 4 : 8); }
+template <class TO> constexpr int tr_vout() { return sizeof(TO) >= 8 ? 2 : (sizeof(TO) == 4 ? 4 : 8); }
+template <class TI> constexpr int tr_tp() { return 32 * tr_vin<TI>(); }
+constexpr int kTrTL = 64;
 
 template <class F, class TO, class TI>
 __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
                                                             TransposeArgs ta, F f) {
-  __shared__ TO tile[kTL][kTP + 1];
-  uint32_t id = blockIdx.x;
+  constexpr int VI = tr_vin<TI>(), VO = tr_vout<TO>();
+  constexpr int TP = tr_tp<TI>(), TL = kTrTL;
+  __shared__ TO tile[TL][TP + 1];
+  const uint32_t id = blockIdx.x;
   const uint32_t bq = fd_div(ta.tilesL, id);
   const uint32_t tl = id - bq * ta.tilesL.d;
   const uint32_t batch = fd_div(ta.tilesP, bq);
   const uint32_t tp = bq - batch * ta.tilesP.d;
   int64_t off[2];
   row_offsets<2>(ta.batch, batch, off);
-  const uint64_t p0 = uint64_t(tp) * kTP, l0 = uint64_t(tl) * kTL;
+  const uint64_t p0 = uint64_t(tp) * TP, l0 = uint64_t(tl) * TL;
   const TI* ab = a + off[1];
   TO* cb = c + off[0];
   const int t = threadIdx.x;
-  // read: lanes run along P (unit stride in the input)
+  // read: 32 lanes x VI elements along P (unit stride in the input), 8 L-rows per pass
   {
-    const int pp = t % kTP;
-    for (int ll = t / kTP; ll < kTL; ll += kBlock / kTP) {
-      const uint64_t p = p0 + pp, l = l0 + ll;
-      if (p < ta.P && l < ta.L) tile[ll][pp] = f(ab[int64_t(l) * ta.in_sL + int64_t(p)]);
+    const int pp = (t % 32) * VI;
+    const uint64_t p = p0 + pp;
+    for (int ll = t / 32; ll < TL; ll += kBlock / 32) {
+      const uint64_t l = l0 + ll;
+      if (l >= ta.L) break;
+      const TI* src = ab + int64_t(l) * ta.in_sL + int64_t(p);
+      if (ta.vec_in && p + VI <= ta.P) {
+        Vec<TI, VI> v = vload<TI, VI>(src);
+#pragma unroll
+        for (int q = 0; q < VI; ++q) tile[ll][pp + q] = f(v.v[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < VI; ++q)
+          if (p + q < ta.P) tile[ll][pp + q] = f(src[q]);
+      }
     }
   }
   __syncthreads();
-  // write: lanes run along L (unit stride in the output)
+  // write: TL/VO lanes x VO elements along L (unit stride in the output)
   {
-    const int ll = t % kTL;
-    for (int pp = t / kTL; pp < kTP; pp += kBlock / kTL) {
-      const uint64_t p = p0 + pp, l = l0 + ll;
-      if (p < ta.P && l < ta.L) cb[int64_t(p) * ta.out_sP + int64_t(l)] = tile[ll][pp];
+    constexpr int LPW = TL / VO;
+    const int ll = (t % LPW) * VO;
+    const uint64_t l = l0 + ll;
+    for (int pp = t / LPW; pp < TP; pp += kBlock / LPW) {
+      const uint64_t p = p0 + pp;
+      if (p >= ta.P) break;
+      TO* dst = cb + int64_t(p) * ta.out_sP + int64_t(l);
+      if (ta.vec_out && l + VO <= ta.L) {
+        Vec<TO, VO> v;
+#pragma unroll
+        for (int q = 0; q < VO; ++q) v.v[q] = tile[ll + q][pp];
+        vstore<TO, VO>(dst, v);
+      } else {
+#pragma unroll
+        for (int q = 0; q < VO; ++q)
+          if (l + q < ta.L) dst[q] = tile[ll + q][pp];
+      }
     }
   }
 }
@@ -270,8 +390,23 @@ __global__ __launch_bounds__(kBlock) void k_binary_generic(const T* __restrict__
   }
 }
 
+template <class F, class TC, class TA, class TB>
+__global__ __launch_bounds__(kBlock) void k_binary_generic_mixed(const TA* __restrict__ a, const TB* __restrict__ b,
+                                                                 TC* __restrict__ c, NdMeta64 m, uint64_t n, F f) {
+  const CastF<TA, TC> ca{};
+  const CastF<TB, TC> cb{};
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += uint64_t(gridDim.x) * kBlock) {
+    int64_t off[3];
+    nd_offsets(m, i, 3, off);
+    c[off[0]] = f(ca(a[off[1]]), cb(b[off[2]]));
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // host side: variant selection
+// vectors per thread: one 16-byte vector per operand per thread (many short blocks) measured best
+// for the flat path on MI355X (6.7 TB/s add at 16M elements); the rows path keeps 4 items
+constexpr int kFlatUnroll = 1;
 constexpr int kUnroll = 4;
 
 template <class T>
@@ -344,8 +479,8 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
     In<TA> ia{a, mode_of(p.stride[1][0])};
     bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a));
     if (vec_ok) {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kUnroll - 1) / (uint64_t(kBlock) * V * kUnroll);
-      k_unary_flat<V, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
+      k_unary_flat<V, kFlatUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
     } else {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
       k_unary_flat<1, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
@@ -365,19 +500,24 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
       ta.L = p.shape[nd - 1];
       ta.in_sL = sL;
       ta.out_sP = p.stride[0][P];
-      uint64_t tL = (ta.L + kTL - 1) / kTL, tP = (ta.P + kTP - 1) / kTP;
+      constexpr uint64_t TP = tr_tp<TA>(), TL = kTrTL;
+      uint64_t tL = (ta.L + TL - 1) / TL, tP = (ta.P + TP - 1) / TP;
       uint64_t nb = p.numel / (ta.P * ta.L);
       if (tL * tP * nb < (uint64_t(1) << 31)) {
         ta.tilesL = make_fastdiv(uint32_t(tL));
         ta.tilesP = make_fastdiv(uint32_t(tP));
         // batch dims: all dims but P and nd-1, innermost first
         ta.batch.nd = 0;
+        ta.vec_in = aligned16(a) && (uint64_t(sL < 0 ? -sL : sL) * sizeof(TA)) % 16 == 0;
+        ta.vec_out = aligned16(c) && (uint64_t(ta.out_sP) * sizeof(TO)) % 16 == 0;
         for (int d = nd - 2; d >= 0; --d) {
           if (d == P) continue;
           int k = ta.batch.nd++;
           ta.batch.div[k] = make_fastdiv(uint32_t(p.shape[d]));
           ta.batch.stride[0][k] = p.stride[0][d];
           ta.batch.stride[1][k] = p.stride[1][d];
+          if ((uint64_t(p.stride[1][d] < 0 ? -p.stride[1][d] : p.stride[1][d]) * sizeof(TA)) % 16) ta.vec_in = false;
+          if ((uint64_t(p.stride[0][d]) * sizeof(TO)) % 16) ta.vec_out = false;
         }
         k_unary_transpose<F, TO, TA><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
         return;
@@ -410,8 +550,8 @@ void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, 
     In<T> ia{a, mode_of(p.stride[1][0])}, ib{b, mode_of(p.stride[2][0])};
     bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a)) && (ib.mode == kModeScalar || aligned16(b));
     if (vec_ok) {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kUnroll - 1) / (uint64_t(kBlock) * V * kUnroll);
-      k_binary_flat<V, kUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
+      k_binary_flat<V, kFlatUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
     } else {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
       k_binary_flat<1, kUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
@@ -426,11 +566,73 @@ void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, 
     uint32_t gpr = (L + V - 1) / V;
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<3> ix = make_row_indexer<3>(p);
+    if (L >= uint32_t(kBlock) * V / 2) {
+      // long rows: column tiles walking down the rows (broadcast operands stay in registers)
+      TileArgs ta{};
+      ta.ix = ix;
+      ta.L = L;
+      ta.rows = uint32_t(p.numel / L);
+      ta.aligned = al;
+      ta.a_inv = ta.b_inv = true;
+      for (int d = 0; d < nd - 1; ++d) {
+        if (p.stride[1][d] != 0) ta.a_inv = false;
+        if (p.stride[2][d] != 0) ta.b_inv = false;
+      }
+      const uint32_t gx = (L + kBlock * V - 1) / (kBlock * V);
+      uint64_t rb = (uint64_t(ta.rows) * gx + 4095) / 4096;  // ~4096 blocks
+      if (rb < 1) rb = 1;
+      if ((ta.rows + rb - 1) / rb > 65535) rb = (ta.rows + 65534) / 65535;
+      ta.rb = uint32_t(rb);
+      const uint32_t gy = uint32_t((ta.rows + rb - 1) / rb);
+      k_binary_tiles<V, F, T><<<dim3(gx, gy), kBlock, 0, st>>>(ia, sa, ib, sb, c, ta, f);
+      return;
+    }
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
     k_binary_rows<V, kUnroll, F, T><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al, f);
     return;
   }
   k_binary_generic<F, T><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
+}
+
+template <class F, class TC, class TA, class TB>
+void launch_binary_mixed(const void* a, const void* b, void* c, int ndim, const size_t* shape, const ssize_t* as,
+                         const ssize_t* bs, hipStream_t st, F f) {
+  Plan p;
+  const ssize_t* ins[2] = {as, bs};
+  if (!plan_elementwise(p, ndim, shape, 2, ins)) return;
+  const TA* pa = static_cast<const TA*>(a);
+  const TB* pb = static_cast<const TB*>(b);
+  TC* pc = static_cast<TC*>(c);
+  constexpr int V = 16 / (sizeof(TA) > sizeof(TB) ? (sizeof(TA) > sizeof(TC) ? sizeof(TA) : sizeof(TC))
+                                                  : (sizeof(TB) > sizeof(TC) ? sizeof(TB) : sizeof(TC)));
+  if (p.ndim == 1 && p.stride[1][0] == 1 && p.stride[2][0] == 1 && aligned16(a) && aligned16(b) && aligned16(c)) {
+    const uint64_t blocks = (p.numel + uint64_t(kBlock) * V - 1) / (uint64_t(kBlock) * V);
+    k_binary_flat_mixed<V, F, TC, TA, TB><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(pa, pb, pc, p.numel, f);
+    return;
+  }
+  k_binary_generic_mixed<F, TC, TA, TB><<<grid_generic(p.numel), kBlock, 0, st>>>(pa, pb, pc, make_meta64(p),
+                                                                                   p.numel, f);
+}
+
+// the (input, input) -> output dtype triples the fused entry point accepts: one input already
+// has the result dtype, the other is int32/int64/f32/f64 (the promotions C3-style data reaches)
+template <class F>
+bool dispatch_mixed(int ta, int tb, int tc, const void* a, const void* b, void* c, int ndim, const size_t* shape,
+                    const ssize_t* as, const ssize_t* bs, hipStream_t st, F f) {
+#define MIX(A, B, C, TA_, TB_, TC_) \
+  if (ta == A && tb == B && tc == C) { launch_binary_mixed<F, TC_, TA_, TB_>(a, b, c, ndim, shape, as, bs, st, f); return true; }
+  MIX(MUSAPY_DT_I64, MUSAPY_DT_F64, MUSAPY_DT_F64, int64_t, double, double)
+  MIX(MUSAPY_DT_F64, MUSAPY_DT_I64, MUSAPY_DT_F64, double, int64_t, double)
+  MIX(MUSAPY_DT_I32, MUSAPY_DT_F64, MUSAPY_DT_F64, int32_t, double, double)
+  MIX(MUSAPY_DT_F64, MUSAPY_DT_I32, MUSAPY_DT_F64, double, int32_t, double)
+  MIX(MUSAPY_DT_I64, MUSAPY_DT_F32, MUSAPY_DT_F32, int64_t, float, float)
+  MIX(MUSAPY_DT_F32, MUSAPY_DT_I64, MUSAPY_DT_F32, float, int64_t, float)
+  MIX(MUSAPY_DT_I32, MUSAPY_DT_F32, MUSAPY_DT_F32, int32_t, float, float)
+  MIX(MUSAPY_DT_F32, MUSAPY_DT_I32, MUSAPY_DT_F32, float, int32_t, float)
+  MIX(MUSAPY_DT_F64, MUSAPY_DT_F32, MUSAPY_DT_F32, double, float, float)
+  MIX(MUSAPY_DT_F32, MUSAPY_DT_F64, MUSAPY_DT_F32, float, double, float)
+#undef MIX
+  return false;
 }
 
 }  // namespace mpy
@@ -516,6 +718,18 @@ void musapy_cast_f32_bf16_v2(const float* a, uint16_t* c, int ndim, const size_t
 void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* as,
                             hipStream_t st) {
   launch_unary<ToF16F, uint16_t, float>(a, c, ndim, shape, as, st, ToF16F{});
+}
+
+int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, int b_dtype, void* c, int c_dtype,
+                           int ndim, const size_t* shape, const ssize_t* as, const ssize_t* bs, hipStream_t st) {
+  switch (op) {
+    case MUSAPY_OP_ADD: return dispatch_mixed(a_dtype, b_dtype, c_dtype, a, b, c, ndim, shape, as, bs, st, AddF{}) ? 0 : -1;
+    case MUSAPY_OP_SUB: return dispatch_mixed(a_dtype, b_dtype, c_dtype, a, b, c, ndim, shape, as, bs, st, SubF{}) ? 0 : -1;
+    case MUSAPY_OP_MUL: return dispatch_mixed(a_dtype, b_dtype, c_dtype, a, b, c, ndim, shape, as, bs, st, MulF{}) ? 0 : -1;
+    case MUSAPY_OP_DIV: return dispatch_mixed(a_dtype, b_dtype, c_dtype, a, b, c, ndim, shape, as, bs, st, DivF{}) ? 0 : -1;
+    case MUSAPY_OP_POW: return dispatch_mixed(a_dtype, b_dtype, c_dtype, a, b, c, ndim, shape, as, bs, st, PowF{}) ? 0 : -1;
+  }
+  return -1;
 }
 
 // stride-aware materialisation of a view (kernels.rs:321-324; u8/u16 are new, for 1- and

@@ -83,6 +83,10 @@ __device__ inline T shfl_xor(T v, int m) {
   return __shfl_xor(v, m, kWave);
 }
 
+// Wrapper-level error of the calling thread (read and cleared by musapy_kernels_take_error):
+// 1 = cumsum scratch missing or too small, 2 = a reduction tile longer than 2^31 elements.
+inline thread_local int g_wrapper_error = 0;
+
 // interleaved complex elements, the ABI types themselves
 using c64 = musapy_c64_t;
 using c128 = musapy_c128_t;

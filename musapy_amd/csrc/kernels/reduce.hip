@@ -19,6 +19,7 @@
 namespace mpy {
 
 constexpr int kRBlock = 256;
+constexpr int kRowBS = 512;  // block size of the block-per-segment row kernel (measured best on MI355X)
 
 // what a kernel writes per (output, tile)
 enum : int { kWriteFinal = 0, kWriteVal = 1, kWritePair = 2 };
@@ -36,13 +37,13 @@ struct RedOut {
 // --------------------------------------------------------------------------------------------
 // Writing one finished accumulator.
 template <class Op, class T, int WRITE>
-__device__ inline void write_result(const RedOut<T>& out, uint64_t slot, typename Op::A acc) {
+__device__ inline void write_result(const RedOut<T>& out, uint64_t slot, typename Op::A acc, int64_t k0 = 0) {
   if constexpr (Op::kOrdered) {
     if constexpr (WRITE == kWritePair) {
       out.val[slot] = acc.idx < 0 ? T(0) : acc.val;
-      out.idx[slot] = acc.idx;
+      out.idx[slot] = acc.idx < 0 ? int64_t(-1) : k0 + int64_t(acc.idx);
     } else if constexpr (Op::kArg) {  // final arg result
-      out.idx[slot] = acc.idx < 0 ? 0 : acc.idx;
+      out.idx[slot] = acc.idx < 0 ? 0 : k0 + int64_t(acc.idx);
     } else {
       // value max/min: an empty tile writes a marker the next level skips
       if (acc.idx < 0)
@@ -104,15 +105,15 @@ struct RowArgs {
   uint64_t nwork;     // out_size * tiles
 };
 
-template <class Op, class T, int GROUP, int VEC, int UNROLL, int WRITE>
-__global__ __launch_bounds__(kRBlock) void k_reduce_row(const T* __restrict__ a, RowArgs ra, RedOut<T> out) {
+template <class Op, class T, int BS, int GROUP, int VEC, int UNROLL, int WRITE>
+__global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowArgs ra, RedOut<T> out) {
   using A = typename Op::A;
-  constexpr int kPer = kRBlock / GROUP;  // items per block
+  constexpr int kPer = BS / GROUP;  // items per block
   const uint64_t w = uint64_t(blockIdx.x) * kPer + threadIdx.x / GROUP;
   const int l = threadIdx.x % GROUP;
   const bool live = w < ra.nwork;
   A acc = Op::init();
-  uint64_t o = 0, t = 0;
+  uint64_t o = 0, t = 0, k0 = 0;
   const T* base = a;
   if (live) {
     o = w / ra.tiles;
@@ -120,40 +121,42 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_row(const T* __restrict__ a,
     int64_t off[1];
     row_offsets<1>(ra.ix, uint32_t(o), off);
     base = a + off[0];
-    uint64_t k0 = t * ra.chunk;
-    uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
-    uint64_t k = k0 + uint64_t(l) * VEC;
-    constexpr uint64_t stepk = uint64_t(GROUP) * VEC;
+    k0 = t * ra.chunk;
+    const uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
+    const T* tb = base + int64_t(k0) * ra.rs;  // indices below are relative to the tile start
+    const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;
+    uint32_t k = uint32_t(l) * VEC;
+    constexpr uint32_t stepk = uint32_t(GROUP) * VEC;
     if (VEC > 1) {
-      for (; k + (UNROLL - 1) * stepk + VEC <= k1; k += UNROLL * stepk) {
+      for (; k + (UNROLL - 1) * stepk + VEC <= n; k += UNROLL * stepk) {
         Vec<T, VEC> x[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(base + k + u * stepk);
+        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(tb + k + u * stepk);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
           for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x[u].v[v], int64_t(k + u * stepk + v));
       }
-      for (; k < k1; k += stepk)
+      for (; k < n; k += stepk)
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
-          if (k + v < k1) acc = Op::step(acc, base[k + v], int64_t(k + v));
+          if (k + v < n) acc = Op::step(acc, tb[k + v], int64_t(k + v));
     } else {
       const int64_t rs = ra.rs;
-      for (; k + (UNROLL - 1) * stepk < k1; k += UNROLL * stepk) {
+      for (; k + (UNROLL - 1) * stepk < n; k += UNROLL * stepk) {
         T x[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = base[int64_t(k + u * stepk) * rs];
+        for (int u = 0; u < UNROLL; ++u) x[u] = tb[int64_t(k + u * stepk) * rs];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
       }
-      for (; k < k1; k += stepk) acc = Op::step(acc, base[int64_t(k) * rs], int64_t(k));
+      for (; k < n; k += stepk) acc = Op::step(acc, tb[int64_t(k) * rs], int64_t(k));
     }
   }
   acc = group_reduce<Op, GROUP>(acc);
   if (live && (GROUP <= kWave ? l == 0 : threadIdx.x == 0)) {
     if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
-    write_result<Op, T, WRITE>(out, w, acc);
+    write_result<Op, T, WRITE>(out, w, acc, int64_t(k0));
   }
 }
 
@@ -201,18 +204,18 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x[u].v[v], int64_t(k + u * kWaves));
+          for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x[u].v[v], int64_t(k + u * kWaves - k0));
       }
       for (; k < k1; k += kWaves) {
         Vec<T, VEC> x = vload<T, VEC>(base + int64_t(k) * ca.rs);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k));
+        for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k - k0));
       }
     } else {
       for (; k < k1; k += kWaves)
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
-          if (c0 + v < ca.C) acc[v] = Op::step(acc[v], base[int64_t(k) * ca.rs + v], int64_t(k));
+          if (c0 + v < ca.C) acc[v] = Op::step(acc[v], base[int64_t(k) * ca.rs + v], int64_t(k - k0));
     }
   }
   if (wv > 0) {
@@ -229,30 +232,31 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       for (int i = 0; i < kWaves - 1; ++i) r = Op::comb(r, part[i][lane * VEC + v]);
       if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, base[v]);
       const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
-      write_result<Op, T, WRITE>(out, o * ca.tiles + t, r);
+      write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
     }
   }
 }
 
 // --------------------------------------------------------------------------------------------
 // pair kernel (arg final / mid): rows of (value, index) partials, contiguous [out][n]
-template <class Op, class T, int WRITE>
+template <class Op, class T, int GROUP, int WRITE>
 __global__ __launch_bounds__(kRBlock) void k_reduce_pairs(const T* __restrict__ pv, const int64_t* __restrict__ pi,
                                                           uint64_t n, uint64_t chunk, uint32_t tiles, uint64_t nwork,
                                                           RedOut<T> out) {
   using A = typename Op::A;
-  const uint64_t w = uint64_t(blockIdx.x) * (kRBlock / kWave) + threadIdx.x / kWave;
-  const int l = threadIdx.x % kWave;
+  const uint64_t w = uint64_t(blockIdx.x) * (kRBlock / GROUP) + threadIdx.x / GROUP;
+  const int l = threadIdx.x % GROUP;
   A acc = Op::init();
   uint64_t o = 0, t = 0;
-  if (w < nwork) {
+  const bool live = w < nwork;
+  if (live) {
     o = w / tiles;
     t = w - o * tiles;
     uint64_t k0 = t * chunk, k1 = k0 + chunk < n ? k0 + chunk : n;
-    for (uint64_t k = k0 + l; k < k1; k += kWave) acc = Op::step_pair(acc, pv[o * n + k], pi[o * n + k]);
+    for (uint64_t k = k0 + l; k < k1; k += GROUP) acc = Op::step_pair(acc, pv[o * n + k], pi[o * n + k]);
   }
-  acc = group_reduce<Op, kWave>(acc);
-  if (w < nwork && l == 0) {
+  acc = group_reduce<Op, GROUP>(acc);
+  if (live && (GROUP <= kWave ? l == 0 : threadIdx.x == 0)) {
     if (t == 0 && is_nan(pv[o * n]) && pi[o * n] >= 0) {  // the level below was absorbed by x[0]
       acc.val = pv[o * n];
       acc.idx = pi[o * n];
@@ -285,20 +289,24 @@ inline RowIndexer<1> out_indexer(const ReducePlan& p, int ndims) {
 // over while each tile still streams a few tens of KB.
 inline size_t tiles_hint(const ReducePlan& p, size_t es) {
   if (p.R <= 1 || p.out_size == 0) return 1;
-  const uint64_t want_items = 2048;
   if (p.kind == kColReduce) {
+    // column tiles: ~512 long-lived blocks (2 per CU) measured best; >= 64 rows per tile
     const int vec = int(16 / es) > 0 ? int(16 / es) : 1;
     uint64_t C = p.oshape[p.ond - 1];
     uint64_t blocks = (p.out_size / C) * ceil_div(C, uint64_t(kWave) * vec);
-    if (blocks >= want_items) return 1;
-    uint64_t tiles = ceil_div(want_items, blocks);
-    uint64_t max_tiles = ceil_div(p.R, 64);  // keep >= 64 rows per tile
+    const uint64_t want_blocks = 512;
+    if (blocks >= want_blocks) return 1;
+    uint64_t tiles = ceil_div(want_blocks, blocks);
+    uint64_t max_tiles = ceil_div(p.R, 64);
     if (tiles > max_tiles) tiles = max_tiles;
     return size_t(tiles < 1 ? 1 : tiles);
   }
-  if (p.out_size >= want_items) return 1;
+  // row segments: one 512-lane block per (output, tile); below ~8K work items a single pass
+  // leaves the GPU idle, so large axes are split into tiles of >= 16 KB
+  const uint64_t want_items = 8192;
+  if (p.out_size >= 2048) return 1;
   uint64_t tiles = ceil_div(want_items, p.out_size);
-  uint64_t max_tiles = ceil_div(p.R * es, 32768);  // >= 32 KB per tile
+  uint64_t max_tiles = ceil_div(p.R * es, 16384);
   if (tiles > max_tiles) tiles = max_tiles;
   return size_t(tiles < 1 ? 1 : tiles);
 }
@@ -310,6 +318,10 @@ void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, con
   if (tiles < 1) tiles = 1;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
+  if (ceil_div(p.R, tiles) >= (uint64_t(1) << 31)) {  // tile-relative indices are 32-bit
+    g_wrapper_error = 2;
+    return;
+  }
   // `tiles` is the caller's partial layout: every slot is written, tiles past the end of the
   // axis hold the operation's "empty" value
   constexpr int V = rvec<T>();
@@ -345,18 +357,18 @@ void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, con
   if (seg >= 4096) {
     unsigned grid = unsigned(ra.nwork);
     if (vec_ok)
-      k_reduce_row<Op, T, kRBlock, V, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+      k_reduce_row<Op, T, kRowBS, kRowBS, V, 4, WRITE><<<grid, kRowBS, 0, st>>>(a, ra, out);
     else
-      k_reduce_row<Op, T, kRBlock, 1, 8, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+      k_reduce_row<Op, T, kRowBS, kRowBS, 1, 8, WRITE><<<grid, kRowBS, 0, st>>>(a, ra, out);
   } else if (seg >= 64) {
     unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock / kWave));
     if (vec_ok)
-      k_reduce_row<Op, T, kWave, V, 2, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+      k_reduce_row<Op, T, kRBlock, kWave, V, 2, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
     else
-      k_reduce_row<Op, T, kWave, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+      k_reduce_row<Op, T, kRBlock, kWave, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
   } else {
     unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock));
-    k_reduce_row<Op, T, 1, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+    k_reduce_row<Op, T, kRBlock, 1, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
   }
 }
 
@@ -375,8 +387,12 @@ void launch_pairs(const T* pv, const int64_t* pi, RedOut<T> out, size_t n, size_
   if (tiles < 1) tiles = 1;
   uint64_t chunk = ceil_div(n, tiles);
   uint64_t nwork = uint64_t(out_size) * tiles;
-  unsigned grid = unsigned(ceil_div(nwork, kRBlock / kWave));
-  k_reduce_pairs<Op, T, WRITE><<<grid, kRBlock, 0, st>>>(pv, pi, n, chunk, uint32_t(tiles), nwork, out);
+  if (chunk >= 2048) {  // long segments: a whole block per (output, tile)
+    k_reduce_pairs<Op, T, kRBlock, WRITE><<<unsigned(nwork), kRBlock, 0, st>>>(pv, pi, n, chunk, uint32_t(tiles), nwork, out);
+  } else {
+    unsigned grid = unsigned(ceil_div(nwork, kRBlock / kWave));
+    k_reduce_pairs<Op, T, kWave, WRITE><<<grid, kRBlock, 0, st>>>(pv, pi, n, chunk, uint32_t(tiles), nwork, out);
+  }
 }
 
 // count produced by "+1" repeated axis_len times in T (cpu_mean_typed, op_builder.rs:3608-3612)
@@ -401,6 +417,8 @@ template <class T> using OpMax = OpExt<T, true, false>;
 template <class T> using OpMin = OpExt<T, false, false>;
 template <class T> using OpArgmax = OpExt<T, true, true>;
 template <class T> using OpArgmin = OpExt<T, false, true>;
+template <class T> using OpArgmax64 = OpExt<T, true, true, int64_t>;  // over (value, absolute index) partials
+template <class T> using OpArgmin64 = OpExt<T, false, true, int64_t>;
 }  // namespace mpy
 
 #define RED_ARGS int ndim, const size_t *in_shape, const ssize_t *in_strides, int axis, size_t axis_len, size_t out_size
@@ -502,15 +520,15 @@ MPY_RED_MEAN(c128, musapy_c128_t, MPY_COUNT_LEN)
   }                                                                                                         \
   void musapy_##NAME##_final_##SN##_v2(const T* partials_val, const int64_t* partials_idx, int64_t* c,      \
                                        size_t num_partials, size_t out_size, hipStream_t st) {              \
-    launch_pairs<OP<T>, T, kWriteFinal>(partials_val, partials_idx, iout<T>(c), num_partials, out_size, 1,  \
-                                        st);                                                                \
+    launch_pairs<OP##64<T>, T, kWriteFinal>(partials_val, partials_idx, iout<T>(c), num_partials, out_size, \
+                                            1, st);                                                         \
   }                                                                                                         \
   void musapy_##NAME##_mid_##SN##_v2(const T* partials_val, const int64_t* partials_idx, T* out_val,        \
                                      int64_t* out_idx, size_t out_size, size_t tiles_per_output,            \
                                      size_t axis_len, hipStream_t st) {                                     \
     RedOut<T> o{out_val, out_idx, 0.0, kFinPlain};                                                          \
-    launch_pairs<OP<T>, T, kWritePair>(partials_val, partials_idx, o, axis_len, out_size, tiles_per_output, \
-                                       st);                                                                 \
+    launch_pairs<OP##64<T>, T, kWritePair>(partials_val, partials_idx, o, axis_len, out_size,               \
+                                           tiles_per_output, st);                                           \
   }
 MPY_RED_ARG(argmax, OpArgmax, i64, int64_t)
 MPY_RED_ARG(argmax, OpArgmax, f32, float)

@@ -41,13 +41,15 @@ __device__ inline c128 acc_shfl(c128 v, int m) {
   return c128{__shfl_xor(v.re, m, kWave), __shfl_xor(v.im, m, kWave)};
 }
 
-template <class T>
+__device__ inline int32_t acc_shfl(int32_t v, int m) { return __shfl_xor(v, m, kWave); }
+
+template <class T, class I>
 struct VI {  // value + index; idx < 0 means "no element yet"
   T val;
-  int64_t idx;
+  I idx;
 };
-template <class T> __device__ inline VI<T> acc_shfl(VI<T> v, int m) {
-  return VI<T>{acc_shfl(v.val, m), acc_shfl(v.idx, m)};
+template <class T, class I> __device__ inline VI<T, I> acc_shfl(VI<T, I> v, int m) {
+  return VI<T, I>{acc_shfl(v.val, m), acc_shfl(v.idx, m)};
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -99,17 +101,20 @@ template <> __device__ inline c128 OpProd<c128>::step(c128 acc, c128 v, int64_t)
 template <> __device__ inline c128 OpProd<c128>::comb(c128 a, c128 b) { return cmul(a, b); }
 
 // ---------------------------------------------------------------------------------------------
-// Ordered family (max / min / argmax / argmin share the accumulator).
-template <class T, bool MAX, bool ARG>
+// Ordered family (max / min / argmax / argmin share the accumulator).  The streaming kernels
+// count I = int32 indices relative to the start of their tile (tiles are < 2^31 elements); the
+// kernels that combine earlier partials carry absolute int64 indices.
+template <class T, bool MAX, bool ARG, class I = int32_t>
 struct OpExt {
-  using A = VI<T>;
+  using A = VI<T, I>;
+  using Idx = I;
   static constexpr bool kOrdered = true;
   static constexpr bool kArg = ARG;
   __device__ static bool better(T a, T b) { return MAX ? (a > b) : (a < b); }
   __device__ static A init() { return A{T(0), -1}; }
   // elements of one lane arrive in increasing k, so a tie never replaces the kept element
   __device__ static A step(A acc, T v, int64_t k) {
-    if (!is_nan(v) && (acc.idx < 0 || better(v, acc.val))) return A{v, k};
+    if (!is_nan(v) && (acc.idx < 0 || better(v, acc.val))) return A{v, I(k)};
     return acc;
   }
   __device__ static A comb(A a, A b) {
@@ -122,7 +127,7 @@ struct OpExt {
   // pair input (partials of an earlier level): (v, k) where k < 0 marks an empty tile
   __device__ static A step_pair(A acc, T v, int64_t k) {
     if (k < 0 || is_nan(v)) return acc;
-    return comb(acc, A{v, k});
+    return comb(acc, A{v, I(k)});
   }
 };
 

@@ -226,6 +226,82 @@ __global__ __launch_bounds__(kSBlock) void k_scan_rows(const T* __restrict__ a, 
   }
 }
 
+// Row scan without look-back, for many rows: block b walks row b tile by tile, keeping the
+// running prefix P in registers and prefetching the next tile while it scans the current one.
+// The in-tile arithmetic and P(c) = P(c-1) + A(c) are exactly those of k_scan_rows, so both
+// kernels produce the same bits.
+template <class T>
+__device__ inline void load_tile(const T* ain, uint64_t k0, uint64_t L, bool vec, typename ScanAcc<T>::A (&x)[scan_items<T>()]) {
+  using A = typename ScanAcc<T>::A;
+  constexpr int N = scan_items<T>();
+  if (vec && k0 + N <= L) {
+    constexpr int VV = int(16 / sizeof(T));
+#pragma unroll
+    for (int j = 0; j < N; j += VV) {
+      Vec<T, VV> v = vload<T, VV>(ain + k0 + j);
+#pragma unroll
+      for (int q = 0; q < VV; ++q) x[j + q] = A(v.v[q]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) x[j] = (k0 + j < L) ? A(ain[k0 + j]) : A(0);
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(kSBlock) void k_scan_rows_seq(const T* __restrict__ a, T* __restrict__ c, RowScanArgs sa) {
+  using A = typename ScanAcc<T>::A;
+  constexpr int N = scan_items<T>();
+  constexpr uint64_t TILE = uint64_t(kSBlock) * N;
+  constexpr int kWaves = kSBlock / kWave;
+  __shared__ A s_wave[2][kWaves];
+  const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+  const uint32_t row = blockIdx.x;
+  int64_t off[2];
+  row_offsets<2>(sa.ix, row, off);
+  const T* ain = a + off[0];
+  T* cout = c + off[1];
+  A x[N], y[N];
+  load_tile<T>(ain, uint64_t(tid) * N, sa.L, sa.vec, x);
+  A P = A(0);
+  for (uint32_t t = 0; t < sa.tiles; ++t) {
+    const uint64_t k0 = uint64_t(t) * TILE + uint64_t(tid) * N;
+    if (t + 1 < sa.tiles) load_tile<T>(ain, k0 + TILE, sa.L, sa.vec, y);
+#pragma unroll
+    for (int j = 1; j < N; ++j) x[j] = x[j - 1] + x[j];
+    A tot = x[N - 1];
+    A incl = wave_incl_scan(tot, lane);
+    if (lane == kWave - 1) s_wave[t & 1][wv] = incl;  // double-buffered: no barrier needed after use
+    __syncthreads();
+    A wave_off = A(0), agg = A(0);
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      if (i < wv) wave_off = wave_off + s_wave[t & 1][i];
+      agg = agg + s_wave[t & 1][i];
+    }
+    A lane_excl = shfl_up_acc(incl, 1);
+    if (lane == 0) lane_excl = A(0);
+    const A local = wave_off + lane_excl;
+    if (sa.vec && k0 + N <= sa.L) {
+      constexpr int VV = int(16 / sizeof(T));
+#pragma unroll
+      for (int j = 0; j < N; j += VV) {
+        Vec<T, VV> v;
+#pragma unroll
+        for (int q = 0; q < VV; ++q) v.v[q] = T(P + (local + x[j + q]));
+        vstore<T, VV>(cout + k0 + j, v);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+        if (k0 + j < sa.L) cout[k0 + j] = T(P + (local + x[j]));
+    }
+    P = P + agg;
+#pragma unroll
+    for (int j = 0; j < N; ++j) x[j] = y[j];
+  }
+}
+
 // one lane per column (or per row for the generic case), sequential along the axis
 struct SeqScanArgs {
   RowIndexer<2> ix;   // dims enumerated by the lane: [0] input, [1] output strides
@@ -260,7 +336,6 @@ __global__ __launch_bounds__(kSBlock) void k_scan_seq(const T* __restrict__ a, T
 }
 
 // ---------------------------------------------------------------------------------------------
-static thread_local int g_scan_error = 0;
 
 template <class T>
 void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
@@ -288,6 +363,11 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
     for (int d = 0; d < p.ond; ++d)
       if (((p.istride[d] * int64_t(sizeof(T))) % 16) || ((p.ostride[d] * int64_t(sizeof(T))) % 16)) vec = false;
     sa.vec = vec;
+    // enough rows to give every CU two of them: walk each row in one block, no look-back
+    if (sa.tiles > 1 && p.rows >= 512) {
+      k_scan_rows_seq<T><<<dim3(sa.rows), kSBlock, 0, st>>>(a, c, sa);
+      return;
+    }
     if (sa.tiles > 1) {
       // tmp capacity per the caller's formula: rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
       uint64_t bpr = (p.L + 255) / 256;
@@ -297,7 +377,7 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
       const uint64_t W = sizeof(T) == 4 ? 1 : 2;
       uint64_t words = 2 + uint64_t(p.rows) * (2 * uint64_t(sa.tiles) - 3) * W;
       if (tmp == nullptr || words * 8 > cap) {
-        g_scan_error = 1;
+        g_wrapper_error = 1;
         return;
       }
       uint64_t* w = reinterpret_cast<uint64_t*>(tmp);
@@ -347,10 +427,11 @@ void musapy_cumsum_f64_v3(const double* a, double* c, double* tmp, int ndim, con
 }
 
 // Returns and clears the calling thread's last wrapper-level error (1 = cumsum scratch missing
-// or too small for the look-back state).  New: the reference wrappers have no such failure mode.
+// or too small for the look-back state, 2 = reduction tile above 2^31 elements).  New: the
+// reference wrappers have no such failure mode.
 int musapy_kernels_take_error(void) {
-  int e = g_scan_error;
-  g_scan_error = 0;
+  int e = g_wrapper_error;
+  g_wrapper_error = 0;
   return e;
 }
 

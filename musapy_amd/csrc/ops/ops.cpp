@@ -264,6 +264,22 @@ Array binary_elementwise(const Array& a, const Array& b, const Array* out, Binar
   }
   check_out(op, out, out_shape, dt, a, "broadcast output shape", "promoted dtype");
   StreamPtr s = pick_stream(a, out);
+  if ((a.dtype != dt || b.dtype != dt) && a.shape() == out_shape && b.shape() == out_shape &&
+      shape_numel(out_shape) > 0) {
+    // promotion without a materialised cast: one fused pass (same bits as cast, then compute)
+    Array r = make_output(out, out_shape, dt, a.device, s, {&a, &b});
+    a.data->wait_last_write_on(s);
+    b.data->wait_last_write_on(s);
+    if (musapy_binary_mixed_v2(int(k), a.data_ptr(), int(a.dtype), b.data_ptr(), int(b.dtype), r.data_ptr(),
+                               int(dt), int(out_shape.size()), out_shape.data(), a.layout.strides.data(),
+                               b.layout.strides.data(), s->raw()) == 0) {
+      check_launch(op);
+      a.data->record_read(s);
+      b.data->record_read(s);
+      r.data->record_write(s);
+      return r;
+    }
+  }
   std::optional<Array> ac, bc;
   if (a.dtype != dt) ac = cast_array(a, dt, s);
   if (b.dtype != dt) bc = cast_array(b, dt, s);
@@ -563,6 +579,48 @@ Array reduce_multi(const Array& a, const std::vector<ssize_t>* axes, bool keepdi
   if (ax.empty()) return reduction_axis(a, std::nullopt, keepdims, out, k);
   if (ax.size() == 1) return reduction_axis(a, ax[0], keepdims, out, k);
   if (out) throw ShapeError("reduction with multiple axes does not support out= yet");
+  if (k == ReduceKernel::Sum || k == ReduceKernel::Prod || k == ReduceKernel::Mean) {
+    // Adjacent reduced axes that one stride walks (e.g. (1,2) of a C-order array) are reduced as
+    // one axis: a single pass instead of one pass per axis.  Only the association of the
+    // floating-point sum/product changes (integer results are identical); max/min/arg keep the
+    // per-axis passes because their NaN and +-0 outcomes depend on that order.  Means merge only
+    // while the merged count is exact in the compute dtype, like the reference's per-axis counts.
+    Dtype ct = reduction_compute_dtype(a.dtype, k);
+    const double count_cap = ct == Dtype::Float32 ? 16777216.0 : 9007199254740992.0;
+    Layout l;
+    l.offset = a.layout.offset;
+    std::vector<size_t> merged_axes;
+    double run_count = 1;
+    for (size_t d = 0; d < a.ndim(); ++d) {
+      const bool red = std::find(ax.begin(), ax.end(), d) != ax.end();
+      const bool prev_red = d > 0 && std::find(ax.begin(), ax.end(), d - 1) != ax.end();
+      const size_t n = a.shape()[d];
+      if (red && prev_red && !l.shape.empty() &&
+          l.strides.back() == a.layout.strides[d] * ssize_t(n) &&
+          (k != ReduceKernel::Mean || run_count * double(n) <= count_cap)) {
+        l.shape.back() *= n;
+        l.strides.back() = a.layout.strides[d];
+        run_count *= double(n);
+        continue;
+      }
+      l.shape.push_back(n);
+      l.strides.push_back(a.layout.strides[d]);
+      run_count = double(n);
+      if (red) merged_axes.push_back(l.shape.size() - 1);
+    }
+    if (merged_axes.size() < ax.size()) {
+      Array v = a.view(l);
+      std::optional<Array> cur;
+      for (size_t x : merged_axes) cur = reduction_axis(cur ? *cur : v, x, true, nullptr, k);
+      Shape target;
+      for (size_t d = 0; d < a.ndim(); ++d) {
+        const bool red = std::find(ax.begin(), ax.end(), d) != ax.end();
+        if (!red) target.push_back(a.shape()[d]);
+        else if (keepdims) target.push_back(1);
+      }
+      return cur->view(Layout::from_shape(target));  // results are C-contiguous
+    }
+  }
   std::optional<Array> cur;
   for (size_t x : ax) cur = reduction_axis(cur ? *cur : a, x, true, nullptr, k);
   if (keepdims) return *cur;

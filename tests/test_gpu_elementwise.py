@@ -96,6 +96,54 @@ def test_binary_empty_and_promotion():
     assert_bits_equal(r.numpy(), R.binary("add", i, f), "i64+f64")
 
 
+MIXED = [(np.int64, np.float64), (np.float64, np.int64), (np.int32, np.float64), (np.float64, np.int32),
+         (np.int64, np.float32), (np.float32, np.int64), (np.int32, np.float32), (np.float32, np.int32),
+         (np.float64, np.float32), (np.float32, np.float64)]
+
+
+def _mixed_operand(dt, shape, op):
+    if np.issubdtype(dt, np.integer):
+        x = RNG.integers(-(2**40) if dt == np.int64 else -(2**30), 2**40 if dt == np.int64 else 2**30, shape)
+        if op == "pow":
+            x = RNG.integers(0, 4, shape)
+        return x.astype(dt)
+    x = RNG.standard_normal(shape) * 1e3
+    if op == "pow":
+        x = np.abs(x) * 1e-3 + 0.5
+    return x.astype(dt)
+
+
+@pytest.mark.parametrize("ta,tb", MIXED)
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "pow"])
+def test_binary_mixed_dtypes_fused(op, ta, tb):
+    """Promotion fused into the arithmetic pass must give the bits of cast-then-compute
+    (dtype.rs:306-334 promotion, op_builder.rs cast then kernel) for every layout."""
+    ulps = 2 if op == "pow" else 0
+    for n in (1, 7, 1023, 4097, (1 << 16) + 3):
+        a, b = _mixed_operand(ta, (n,), op), _mixed_operand(tb, (n,), op)
+        got = getattr(ms, op)(dev(a), dev(b)).numpy()
+        check_float(got, R.binary(op, a, b), ulps, f"{op} {ta.__name__}+{tb.__name__} n={n}")
+    a, b = _mixed_operand(ta, (40, 24), op), _mixed_operand(tb, (24, 40), op)
+    got = getattr(ms, op)(dev(a), ms.transpose(dev(b))).numpy()
+    check_float(got, R.binary(op, a, np.ascontiguousarray(b.T)), ulps, f"{op} {ta.__name__}+{tb.__name__} T")
+    # unaligned start: slice off the first element of both operands
+    a, b = _mixed_operand(ta, (1001,), op), _mixed_operand(tb, (1001,), op)
+    got = getattr(ms, op)(ms.slice(dev(a), [(1, 1001, 1)]), ms.slice(dev(b), [(1, 1001, 1)])).numpy()
+    check_float(got, R.binary(op, a[1:], b[1:]), ulps, f"{op} {ta.__name__}+{tb.__name__} offset")
+
+
+def test_binary_mixed_broadcast_and_out():
+    a = RNG.integers(-1000, 1000, (300, 1)).astype(np.int64)
+    b = RNG.standard_normal((300, 257))
+    assert_bits_equal(ms.add(dev(a), dev(b)).numpy(), R.binary("add", a, b), "i64 col + f64 broadcast")
+    a = RNG.integers(-1000, 1000, (300, 257)).astype(np.int32)
+    b = RNG.standard_normal((300, 257)).astype(np.float32)
+    out = ms.from_numpy(np.zeros((300, 257), np.float32))
+    r = ms.mul(dev(a), dev(b), out=out)
+    assert_bits_equal(out.numpy(), R.binary("mul", a, b), "i32*f32 out=")
+    assert r.shape == (300, 257)
+
+
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 @pytest.mark.parametrize("op", ["sin", "cos", "exp", "log", "abs", "sign", "neg"])
 def test_unary_layouts(op, dt):

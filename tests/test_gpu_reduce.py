@@ -121,6 +121,29 @@ def test_multi_axis(kind):
             check_reduce(kind, x, axes, keep)
 
 
+@pytest.mark.parametrize("kind", ["sum", "mean", "prod"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_multi_axis_merged(kind, dt):
+    """Adjacent reduced axes that are stride-contiguous are reduced in one pass; the result
+    must stay within the bound of the reference's axis-by-axis order."""
+    shape = (24, 96, 130)
+    if kind == "prod":
+        x = RNG.uniform(0.999, 1.001, shape) if dt != np.int64 else RNG.integers(-1, 2, shape)
+    else:
+        x = RNG.standard_normal(shape) * 100 if dt != np.int64 else RNG.integers(-(2**40), 2**40, shape)
+    x = x.astype(dt)
+    if kind == "mean" and dt == np.int64:
+        x = x.astype(np.float64)
+    for axes in ((1, 2), (0, 1), (0, 1, 2), (-2, -1)):
+        for keep in (False, True):
+            check_reduce(kind, x, axes, keep)
+    # a permuted view: reduced axes no longer stride-contiguous, reduced one at a time
+    xt = np.ascontiguousarray(np.transpose(x, (2, 0, 1)))
+    gx = ms.permute(dev(x), (2, 0, 1))
+    for axes in ((0, 1), (1, 2)):
+        check_reduce(kind, xt, axes, gpu_x=gx)
+
+
 @pytest.mark.parametrize("dt", [np.complex64, np.complex128])
 def test_complex_reductions(dt):
     for shape, axes in (((3, 4), [None, 0, 1, (0, 1), -1]), ((16, 64, 64), [(1, 2), 0, 2]), ((4, 200000), [1])):
