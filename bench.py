@@ -12,13 +12,14 @@ over 4 device copies, so every launch streams its inputs from HBM rather than fr
 Infinity Cache.  `value` = algorithmic bytes of the step / summed average launch time.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
 musapy's CPU path) on the same step.
 
-    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu] [--only add|sum|argmax|copy]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -34,7 +35,29 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--all", action="store_true", help="also time every BASELINE config (table on stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", choices=["add", "sum", "argmax", "copy"],
+                   help="launch one step op (or the calibration copy) warmup+steps times and exit; "
+                        "the program run under rocprofv3 --pmc for the HBM traffic figures")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_step_kernels.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of each step kernel, from the committed rocprofv3 --pmc summary:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one pass each) scaled by what the same counters
+    read for a plain copy of known size.  Rows look like `| key | kernel | ... | bytes |`."""
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"\|\s*(add|sum|argmax)\s*\|.*\|\s*([0-9]+)\s*\|\s*$", line)
+                if m:
+                    out[m.group(1)] = int(m.group(2))
+    except OSError:
+        pass
+    return out
 
 
 COPIES = 4  # input copies rotated between launches (4 x the working set >> the 256 MB MALL)
@@ -72,10 +95,17 @@ def step_ops(ms):
     I = ms.from_numpy(np.zeros(8192, np.int64))
     n = 8192 * 8192
     ops = [
-        ("C1 add f32 16,777,216", lambda i: ms.add(A[i % COPIES], B[i % COPIES], out=C), 12 * 16_777_216),
-        ("C4 sum axis=-1 (8192,8192) f32", lambda i: ms.sum(X[i % COPIES], axis=-1, out=S), 4 * n + 4 * 8192),
-        ("C4 argmax axis=1 (8192,8192) f32", lambda i: ms.argmax(X[i % COPIES], axis=1, out=I), 4 * n + 8 * 8192),
+        ("add", "C1 add f32 16,777,216", lambda i: ms.add(A[i % COPIES], B[i % COPIES], out=C), 12 * 16_777_216),
+        ("sum", "C4 sum axis=-1 (8192,8192) f32", lambda i: ms.sum(X[i % COPIES], axis=-1, out=S),
+         4 * n + 4 * 8192),
+        ("argmax", "C4 argmax axis=1 (8192,8192) f32", lambda i: ms.argmax(X[i % COPIES], axis=1, out=I),
+         4 * n + 8 * 8192),
     ]
+    # calibration: a plain copy of a unit-stride view starting 4 KiB in (page- and line-aligned,
+    # so no cache line is shared between workgroups): one vectorised copy kernel
+    m = 16_777_216 - 1024
+    ops.append(("copy", "calibration copy f32 16,776,192",
+                lambda i: ms.contiguous(ms.slice(A[i % COPIES], [(1024, 16_777_216, 1)])), 8 * m))
     host = {"a": a, "b": b, "x": x}
     return ops, host
 
@@ -157,7 +187,16 @@ def main():
 
     timer = Timer(ms)
     ops, host = step_ops(ms)
-    for name, fn, _ in ops:  # warm-up (first launches load code objects, fill the memory pool)
+    if args.only:
+        key, name, fn, bytes_ = next(o for o in ops if o[0] == args.only)
+        for i in range(args.warmup + args.steps):
+            fn(i)
+        ms.synchronize()
+        print(json.dumps({"only": key, "op": name, "launches": args.warmup + args.steps, "algo_bytes": bytes_}),
+              flush=True)
+        return
+    ops = [o for o in ops if o[0] != "copy"]
+    for _, name, fn, _ in ops:  # warm-up (first launches load code objects, fill the memory pool)
         for i in range(max(args.warmup, 1)):
             fn(i)
     ms.synchronize()
@@ -166,19 +205,22 @@ def main():
     ms.synchronize()
     # K steps: each op is launched K times back-to-back between two events (inputs rotate over
     # COPIES device copies, so every launch streams from HBM)
-    for name, fn, _ in ops:
+    for _, name, fn, _ in ops:
         per_op[name] = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(args.steps)])
     ms.synchronize()
     wall = time.perf_counter() - t0
     table = {}
+    keys = {}
     total_bytes, total_ms = 0, 0.0
-    for name, fn, bytes_ in ops:
+    for key, name, fn, bytes_ in ops:
         t = float(per_op[name])
         table[name] = {"ms": round(t, 5), "algo_bytes": bytes_, "GBps": round(bytes_ / t / 1e6, 1),
                        "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4)}
+        keys[name] = key
         total_bytes += bytes_
         total_ms += t
     dom = max(table, key=lambda k: table[k]["ms"])
+    traffic = measured_traffic().get(keys[dom])
     value = total_bytes / total_ms / 1e6
     line = {
         "metric": "achieved HBM GB/s (and % of MI355X peak) for f32 add, axis-sum, argmax",
@@ -200,7 +242,10 @@ def main():
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "ops": table,
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["GBps"], "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": None},
+                     "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": traffic,
+                     "algo_bytes": table[dom]["algo_bytes"],
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, os.path.dirname(os.path.abspath(__file__)))
+                     if traffic is not None else None},
     }
     if not args.no_cpu:
         v, sec, sample = cpu_baseline(host)
