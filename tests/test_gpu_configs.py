@@ -86,6 +86,9 @@ def test_c5_cumsum_and_complex_sum():
     got = ms.cumsum(dev(y), axis=1).numpy()
     want = R.cumsum(y, 1)
     assert np.all(np.abs(got - want) <= 1e-12 * np.abs(want))
+    # size-independent properties: prefixes of U(0,1) data never decrease, the last prefix is the row sum
+    assert np.all(np.diff(got, axis=1) >= 0)
+    assert np.all(np.abs(got[:, -1] - R.reduce(y, "sum", 1)) <= 1e-12 * got[:, -1])
     rng = np.random.default_rng(0)
     re = rng.standard_normal((16, 1024, 1024), dtype=np.float32)
     im = rng.standard_normal((16, 1024, 1024), dtype=np.float32)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from oracle import reference as R
-from tests.conftest import assert_bits_equal, ulp_diff_f32
+from tests.conftest import assert_bits_equal, ulp_diff_f32, ulp_diff_f64
 
 RNG = np.random.default_rng(1234)
 
@@ -74,6 +74,15 @@ def test_unary_transcendental_f32_close_to_exact(op, fn):
     x = RNG.uniform(0.01 if op == "log" else -20, 20, 20000).astype(np.float32)
     got = R.unary(op, x)
     assert ulp_diff_f32(got, _exact_f32(fn, x)).max() <= 1
+
+
+@pytest.mark.parametrize("op,fn", [("sin", np.sin), ("cos", np.cos), ("exp", np.exp), ("log", np.log)])
+def test_unary_transcendental_f64_close_to_exact(op, fn):
+    """f64 forms against x87 extended precision (64-bit mantissa), rounded once to double."""
+    x = RNG.uniform(0.01 if op == "log" else -20, 20, 20000)
+    got = R.unary(op, x)
+    want = fn(x.astype(np.longdouble)).astype(np.float64)
+    assert ulp_diff_f64(got, want).max() <= 1
 
 
 def test_unary_exact_ops():
