@@ -7,9 +7,12 @@
  *   rust/musapy-core/src/buffer_pool.rs:51-170    size-class cache of device buffers
  *   rust/musapy-core/src/deferred_free.rs:55-138  free-after-sync queue
  *   rust/musapy-core/src/mem_stats.rs:18-114      allocation counters
- * Device memory comes from hipMallocAsync on the device's default memory pool with an unlimited
- * release threshold: frees are stream-ordered (no deferred-free queue is needed) and freed
- * blocks are recycled by the pool.  All functions return 0 on success or a hipError_t code.
+ * Device memory comes from a stream-aware caching allocator: sizes round up to 8 classes per
+ * power of two, a freed block is cached with the stream its free was ordered on, reuse on that
+ * stream is immediate and host-only, reuse from another stream is ordered by an event, and a
+ * miss calls hipMalloc (after returning the cache to the device when memory runs out).  No call
+ * blocks the host on device work except the copies to/from host memory and the synchronizes.
+ * All functions return 0 on success or a hipError_t code (negative: a kernel-wrapper error).
  * Streams are always created with the default priority.
  */
 #ifndef MUSAPY_HIP_RUNTIME_H
@@ -31,9 +34,16 @@ int mpy_rt_set_device(int device);
 int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_mem, int* cu_count, int* arch_major,
                        int* arch_minor);
 
-/* stream-ordered allocation on `device` (pool-backed); `stream` may be NULL (null stream) */
+/* stream-ordered allocation on `device` (cached); `stream` may be NULL (null stream).  The block
+ * may be used by work on `stream` right away; a free is ordered after the work queued on the
+ * stream it names. */
 int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream);
 int mpy_rt_free(void* ptr, hipStream_t stream);
+/* returns the cached (freed, unused) blocks of `device` (all devices when < 0) to the device;
+ * synchronizes the device first */
+int mpy_rt_empty_cache(int device);
+/* bytes held in the cache of `device` (all devices when < 0) */
+size_t mpy_rt_mem_cached(int device);
 
 int mpy_rt_memcpy_h2d(void* dst, const void* src, size_t nbytes, hipStream_t stream);
 int mpy_rt_memcpy_d2h(void* dst, const void* src, size_t nbytes, hipStream_t stream);
@@ -52,7 +62,8 @@ int mpy_rt_event_synchronize(hipEvent_t event);
 int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop);
 
 /* After a kernel-ABI call: returns the pending launch error (hipGetLastError) or, if none, the
- * kernel library's own wrapper error (musapy_kernels_take_error, mapped to -1). */
+ * kernel library's own wrapper error negated (musapy_kernels_take_error: -1 cumsum scratch,
+ * -2 reduction tile too long). */
 int mpy_rt_check_launch(void);
 const char* mpy_rt_error_string(int code);
 

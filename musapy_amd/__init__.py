@@ -17,7 +17,7 @@ try:
     from . import _core
 except ImportError as _e:  # pragma: no cover - exercised only on an unbuilt tree
     raise ImportError(
-        "musapy_amd native extension is not built (run `python -m musapy_amd.build`): " + str(_e)
+        "musapy_amd native extension is not built (run `python musapy_amd/build.py`): " + str(_e)
     ) from _e
 
 from ._core import (  # noqa: F401
@@ -26,7 +26,7 @@ from ._core import (  # noqa: F401
     add, sub, mul, div, pow, sin, cos, exp, log, abs, sign, neg, clamp, astype,
     sum, prod, max, min, mean, argmax, argmin, cumsum,
     transpose, flip, index_select, contiguous,
-    set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats,
+    set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats, empty_cache,
 )
 
 __all__ = [

@@ -5,7 +5,7 @@
 * ``musapy_amd/_core*.so`` -- the C++ op layer and its pybind11 binding, linked against the
   library above (rpath $ORIGIN).
 
-Run ``python -m musapy_amd.build`` (or ``__graft_entry__.build()``).  Every call recompiles.
+Run ``python musapy_amd/build.py`` (or ``__graft_entry__.build()``).  Every call recompiles.
 """
 from __future__ import annotations
 

@@ -51,14 +51,14 @@ __global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict_
         for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
     } else {
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) va[u] = vload<TA, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
+      for (int u = 0; u < UNROLL; ++u) va[u] = vload_nt<TA, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k]);
-      vstore<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+      vstore_out<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
     }
   } else {
     for (uint64_t i = base + t; i < n; i += kBlock) c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i]);
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __r
         for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
     } else {
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) va[u] = vload<T, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
+      for (int u = 0; u < UNROLL; ++u) va[u] = vload_nt<T, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC);
     }
     if (b.mode == kModeScalar) {
       const T s = b.p[0];
@@ -90,14 +90,14 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __r
         for (int k = 0; k < VEC; ++k) vb[u].v[k] = s;
     } else {
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) vb[u] = vload<T, VEC>(b.p + base + uint64_t(u * kBlock + t) * VEC);
+      for (int u = 0; u < UNROLL; ++u) vb[u] = vload_nt<T, VEC>(b.p + base + uint64_t(u * kBlock + t) * VEC);
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       Vec<T, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k], vb[u].v[k]);
-      vstore<T, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+      vstore_out<T, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
     }
   } else {
     for (uint64_t i = base + t; i < n; i += kBlock)
@@ -109,7 +109,9 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __r
 // rows: output rows of length L (the innermost coalesced dim).  A work item is VEC consecutive
 // elements of one row; `aligned` (host-checked) guarantees every item is full and every
 // unit-stride operand is 16-byte aligned at the item start.
-template <int VEC, class T>
+// STREAM: the operand is read once per launch (streaming load); false for operands that every
+// block re-reads (broadcast rows).
+template <int VEC, class T, bool STREAM = true>
 __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t col, uint32_t L, bool full,
                                  T (&x)[VEC]) {
   if (mode == kModeScalar) {
@@ -117,7 +119,7 @@ __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t co
 #pragma unroll
     for (int k = 0; k < VEC; ++k) x[k] = v;
   } else if (mode == kModeUnit && full) {
-    Vec<T, VEC> v = vload<T, VEC>(base + col);
+    Vec<T, VEC> v = STREAM ? vload_nt<T, VEC>(base + col) : vload<T, VEC>(base + col);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) x[k] = v.v[k];
   } else {
@@ -147,7 +149,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k]);
-      vstore<TO, VEC>(cp, v);
+      vstore_out<TO, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
       Vec<T, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k], y[k]);
-      vstore<T, VEC>(cp, v);
+      vstore_out<T, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -197,12 +199,12 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restri
   const CastF<TA, TC> ca{};
   const CastF<TB, TC> cb{};
   if (i0 + VEC <= n) {
-    Vec<TA, VEC> x = vload<TA, VEC>(a + i0);
-    Vec<TB, VEC> y = vload<TB, VEC>(b + i0);
+    Vec<TA, VEC> x = vload_nt<TA, VEC>(a + i0);
+    Vec<TB, VEC> y = vload_nt<TB, VEC>(b + i0);
     Vec<TC, VEC> z;
 #pragma unroll
     for (int k = 0; k < VEC; ++k) z.v[k] = f(ca(x.v[k]), cb(y.v[k]));
-    vstore<TC, VEC>(c + i0, z);
+    vstore_out<TC, VEC>(c + i0, z);
   } else {
     for (uint64_t i = i0; i < n; ++i) c[i] = f(ca(a[i]), cb(b[i]));
   }
@@ -230,8 +232,8 @@ __global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In
   const uint32_t r0 = blockIdx.y * ta.rb;
   const uint32_t r1 = r0 + ta.rb < ta.rows ? r0 + ta.rb : ta.rows;
   T ia[VEC], ib[VEC];  // row-invariant operands
-  if (ta.a_inv) load_item<VEC, T>(a.p, a.mode, sa, col, ta.L, vec, ia);
-  if (ta.b_inv) load_item<VEC, T>(b.p, b.mode, sb, col, ta.L, vec, ib);
+  if (ta.a_inv) load_item<VEC, T, false>(a.p, a.mode, sa, col, ta.L, vec, ia);
+  if (ta.b_inv) load_item<VEC, T, false>(b.p, b.mode, sb, col, ta.L, vec, ib);
   constexpr int RU = 4;  // rows whose loads are issued before their stores
   for (uint32_t r = r0; r < r1; r += RU) {
     T xa[RU][VEC], xb[RU][VEC];
@@ -263,7 +265,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In
         Vec<T, VEC> v;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) v.v[k] = f(xa[u][k], xb[u][k]);
-        vstore<T, VEC>(cp, v);
+        vstore_out<T, VEC>(cp, v);
       } else {
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
       if (l >= ta.L) break;
       const TI* src = ab + int64_t(l) * ta.in_sL + int64_t(p);
       if (ta.vec_in && p + VI <= ta.P) {
-        Vec<TI, VI> v = vload<TI, VI>(src);
+        Vec<TI, VI> v = vload_nt<TI, VI>(src);
 #pragma unroll
         for (int q = 0; q < VI; ++q) tile[ll][pp + q] = f(v.v[q]);
       } else {
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
         Vec<TO, VO> v;
 #pragma unroll
         for (int q = 0; q < VO; ++q) v.v[q] = tile[ll + q][pp];
-        vstore<TO, VO>(dst, v);
+        vstore_out<TO, VO>(dst, v);
       } else {
 #pragma unroll
         for (int q = 0; q < VO; ++q)

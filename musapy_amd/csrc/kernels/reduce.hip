@@ -131,7 +131,7 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
       for (; k + (UNROLL - 1) * stepk + VEC <= n; k += UNROLL * stepk) {
         Vec<T, VEC> x[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(tb + k + u * stepk);
+        for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<T, VEC>(tb + k + u * stepk);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
@@ -200,14 +200,14 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       for (; k + (UNROLL - 1) * kWaves < k1; k += UNROLL * kWaves) {
         Vec<T, VEC> x[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = vload<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs);
+        for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
           for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x[u].v[v], int64_t(k + u * kWaves - k0));
       }
       for (; k < k1; k += kWaves) {
-        Vec<T, VEC> x = vload<T, VEC>(base + int64_t(k) * ca.rs);
+        Vec<T, VEC> x = vload_nt<T, VEC>(base + int64_t(k) * ca.rs);
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k - k0));
       }

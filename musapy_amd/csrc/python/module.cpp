@@ -257,8 +257,11 @@ PYBIND11_MODULE(_core, m) {
     r["live_bytes"] = live;
     r["peak_bytes"] = peak;
     r["num_allocs"] = n;
+    r["cached_bytes"] = mpy_rt_mem_cached(-1);
     return r;
   });
+  m.def("empty_cache", [](int device) { check_rt(mpy_rt_empty_cache(device), "empty cache"); },
+        py::arg("device") = -1);
 
   // measurement hooks: HIP events recorded on the device's stream, and a plain fill kernel
   // (used by bench.py to evict the Infinity Cache between timed launches)

@@ -1,16 +1,31 @@
 // hip_runtime.cpp -- the C-ABI HIP runtime layer (include/musapy_hip_runtime.h).
 //
 // Stands in for rust/musapy-core/src/{musa_ffi,buffer_pool,deferred_free,mem_stats}.rs.
-// Allocation is stream-ordered (hipMallocAsync) from the device's default pool whose release
-// threshold is raised to "never", so freed blocks stay cached for reuse the way the reference's
-// buffer pool keeps them (buffer_pool.rs:74-148), but reuse is ordered by the stream instead of
-// by events.  If a device reports no memory-pool support, plain hipMalloc/hipFree are used.
+//
+// Device memory comes from a stream-aware caching allocator, the counterpart of the reference's
+// size-class buffer pool (buffer_pool.rs:51-170) and its free-after-sync queue
+// (deferred_free.rs:55-138):
+//   * sizes are rounded up to one of 8 classes per power of two (at most 12.5% slack; 512 B
+//     minimum), and a freed block goes to a per-device free list tagged with the stream its free
+//     was ordered on;
+//   * an allocation on that same stream reuses the block at once -- stream order already puts the
+//     new work after every earlier use -- with no HIP call at all;
+//   * reuse from another stream first makes the allocating stream wait on an event recorded on
+//     the freeing stream;
+//   * a miss calls hipMalloc; when that runs out of memory, the cache is returned to the device
+//     (after a device synchronize) and the allocation is tried once more.
+// hipMallocAsync/hipFreeAsync on the default memory pool were measured to block the host until
+// the device drains (host time per op equal to its GPU time), which is what this avoids.
+// All functions return 0 on success or a hipError_t code.  Streams are always created with the
+// default priority.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../../include/musapy_hip_runtime.h"
 
@@ -18,38 +33,34 @@ extern "C" int musapy_kernels_take_error(void);
 
 namespace {
 
-std::atomic<size_t> g_live{0}, g_peak{0}, g_count{0};
-std::mutex g_mu;
-std::unordered_map<void*, size_t> g_sizes;  // live allocation sizes (for the counters)
-int g_pool_state[64] = {0};                 // 0 unknown, 1 pool configured, 2 no pool support
+constexpr int kMaxDevices = 64;
 
-int ensure_pool(int device) {
-  if (device < 0 || device >= 64) return int(hipErrorInvalidDevice);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (g_pool_state[device] != 0) return 0;
-  int supported = 0;
-  hipError_t e = hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, device);
-  if (e != hipSuccess || !supported) {
-    g_pool_state[device] = 2;
-    return 0;
-  }
-  hipMemPool_t pool;
-  e = hipDeviceGetDefaultMemPool(&pool, device);
-  if (e != hipSuccess) {
-    g_pool_state[device] = 2;
-    return 0;
-  }
-  uint64_t threshold = UINT64_MAX;
-  e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
-  g_pool_state[device] = (e == hipSuccess) ? 1 : 2;
-  return 0;
+struct Block {
+  void* ptr;
+  size_t size;         // size class actually allocated
+  size_t requested;    // bytes the caller asked for (statistics)
+  hipStream_t stream;  // stream the last free was ordered on (or the owner while live)
+  bool idle;           // no work can be pending on it (its stream was synchronized and destroyed)
+};
+
+struct DevicePool {
+  std::multimap<size_t, Block> free;         // size class -> cached blocks
+  std::unordered_map<void*, Block> live;     // blocks held by callers
+  size_t cached_bytes = 0;
+};
+
+std::mutex g_mu;
+DevicePool g_pools[kMaxDevices];
+std::atomic<size_t> g_live{0}, g_peak{0}, g_count{0};
+
+size_t size_class(size_t n) {
+  if (n <= 512) return 512;
+  const int lg = 63 - __builtin_clzll(uint64_t(n - 1));  // n - 1 >= 512, so lg >= 9
+  const size_t step = size_t(1) << (lg - 3);
+  return (n + step - 1) / step * step;
 }
 
-void note_alloc(void* p, size_t n) {
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    g_sizes[p] = n;
-  }
+void note_alloc(size_t n) {
   size_t live = g_live.fetch_add(n) + n;
   size_t peak = g_peak.load();
   while (live > peak && !g_peak.compare_exchange_weak(peak, live)) {
@@ -57,17 +68,31 @@ void note_alloc(void* p, size_t n) {
   g_count.fetch_add(1);
 }
 
-void note_free(void* p) {
-  size_t n = 0;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_sizes.find(p);
-    if (it != g_sizes.end()) {
-      n = it->second;
-      g_sizes.erase(it);
-    }
-  }
-  g_live.fetch_sub(n);
+// make `waiter` wait for everything queued so far on `target`
+hipError_t order_after(hipStream_t waiter, hipStream_t target) {
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return e;
+  e = hipEventRecord(ev, target);
+  if (e == hipSuccess) e = hipStreamWaitEvent(waiter, ev, 0);
+  hipEventDestroy(ev);
+  return e;
+}
+
+// returns every cached block of `device` to the device; the caller holds g_mu
+hipError_t release_cached_locked(int device) {
+  DevicePool& P = g_pools[device];
+  if (P.free.empty()) return hipSuccess;
+  int prev = 0;
+  hipGetDevice(&prev);
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return e;
+  e = hipDeviceSynchronize();  // frees were stream-ordered: their work must be done
+  for (auto& kv : P.free) hipFree(kv.second.ptr);
+  P.free.clear();
+  P.cached_bytes = 0;
+  hipSetDevice(prev);
+  return e;
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
@@ -100,30 +125,82 @@ int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_me
 
 int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
   *ptr = nullptr;
-  if (nbytes == 0) nbytes = 1;  // a valid, unique pointer even for empty arrays
+  if (device < 0 || device >= kMaxDevices) return int(hipErrorInvalidDevice);
+  const size_t cls = size_class(nbytes ? nbytes : 1);  // a valid, unique pointer even for empty arrays
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevicePool& P = g_pools[device];
+  auto range = P.free.equal_range(cls);
+  if (range.first != range.second) {
+    auto pick = range.first;  // prefer a block freed on this stream or one with nothing pending
+    for (auto it = range.first; it != range.second; ++it)
+      if (it->second.idle || it->second.stream == stream) {
+        pick = it;
+        break;
+      }
+    Block b = pick->second;
+    if (!b.idle && b.stream != stream) {
+      hipError_t e = order_after(stream, b.stream);
+      if (e != hipSuccess) return int(e);
+    }
+    P.free.erase(pick);
+    P.cached_bytes -= b.size;
+    b.stream = stream;
+    b.idle = false;
+    b.requested = nbytes;
+    P.live[b.ptr] = b;
+    note_alloc(nbytes);
+    *ptr = b.ptr;
+    return 0;
+  }
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return int(e);
-  ensure_pool(device);
-  if (g_pool_state[device] == 1)
-    e = hipMallocAsync(ptr, nbytes, stream);
-  else
-    e = hipMalloc(ptr, nbytes);
+  void* p = nullptr;
+  e = hipMalloc(&p, cls);
+  if (e == hipErrorOutOfMemory) {
+    (void)hipGetLastError();
+    for (int d = 0; d < kMaxDevices; ++d)
+      if (!g_pools[d].free.empty()) release_cached_locked(d);
+    hipSetDevice(device);
+    e = hipMalloc(&p, cls);
+  }
   if (e != hipSuccess) {
-    *ptr = nullptr;
+    (void)hipGetLastError();  // leave no sticky error for the next launch check
     return int(e);
   }
-  note_alloc(*ptr, nbytes);
+  P.live[p] = Block{p, cls, nbytes, stream, false};
+  note_alloc(nbytes);
+  *ptr = p;
   return 0;
 }
 
 int mpy_rt_free(void* ptr, hipStream_t stream) {
   if (!ptr) return 0;
-  note_free(ptr);
-  hipPointerAttribute_t attr;
-  int device = 0;
-  if (hipPointerGetAttributes(&attr, ptr) == hipSuccess) device = attr.device;
-  if (device >= 0 && device < 64 && g_pool_state[device] == 1) return int(hipFreeAsync(ptr, stream));
-  return int(hipFree(ptr));
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int d = 0; d < kMaxDevices; ++d) {
+    DevicePool& P = g_pools[d];
+    auto it = P.live.find(ptr);
+    if (it == P.live.end()) continue;
+    Block b = it->second;
+    P.live.erase(it);
+    g_live.fetch_sub(b.requested);
+    b.stream = stream;
+    b.idle = false;
+    P.free.emplace(b.size, b);
+    P.cached_bytes += b.size;
+    return 0;
+  }
+  return int(hipFree(ptr));  // not from this allocator
+}
+
+int mpy_rt_empty_cache(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (device >= 0) return device < kMaxDevices ? int(release_cached_locked(device)) : int(hipErrorInvalidDevice);
+  hipError_t first = hipSuccess;
+  for (int d = 0; d < kMaxDevices; ++d) {
+    hipError_t e = release_cached_locked(d);
+    if (first == hipSuccess) first = e;
+  }
+  return int(first);
 }
 
 int mpy_rt_memcpy_h2d(void* dst, const void* src, size_t n, hipStream_t s) {
@@ -148,7 +225,22 @@ int mpy_rt_stream_create(hipStream_t* stream, int device) {
   if (e != hipSuccess) return int(e);
   return int(hipStreamCreateWithFlags(stream, hipStreamNonBlocking));
 }
-int mpy_rt_stream_destroy(hipStream_t stream) { return int(hipStreamDestroy(stream)); }
+int mpy_rt_stream_destroy(hipStream_t stream) {
+  // cached blocks last freed on this stream outlive it: drain it, then mark them idle so no
+  // later reuse records an event on the destroyed handle
+  hipError_t e = hipStreamSynchronize(stream);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (int d = 0; d < kMaxDevices; ++d) {
+      for (auto& kv : g_pools[d].free)
+        if (kv.second.stream == stream) kv.second.idle = true;
+      for (auto& kv : g_pools[d].live)
+        if (kv.second.stream == stream) kv.second.idle = true;
+    }
+  }
+  hipError_t e2 = hipStreamDestroy(stream);
+  return int(e != hipSuccess ? e : e2);
+}
 int mpy_rt_stream_synchronize(hipStream_t stream) { return int(hipStreamSynchronize(stream)); }
 int mpy_rt_device_synchronize(void) { return int(hipDeviceSynchronize()); }
 
@@ -164,11 +256,14 @@ int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t a, hipEvent_t b) { return int(
 int mpy_rt_check_launch(void) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return int(e);
-  return musapy_kernels_take_error() ? -1 : 0;
+  const int w = musapy_kernels_take_error();
+  return w ? -w : 0;
 }
 
 const char* mpy_rt_error_string(int code) {
-  if (code == -1) return "kernel wrapper error: scratch buffer missing or too small";
+  if (code == -1) return "kernel wrapper error: cumsum scratch buffer missing or too small";
+  if (code == -2) return "kernel wrapper error: a reduction tile reaches 2^31 elements (pass more tiles)";
+  if (code < 0) return "kernel wrapper error";
   return hipGetErrorString(hipError_t(code));
 }
 
@@ -176,6 +271,14 @@ void mpy_rt_mem_stats(size_t* live, size_t* peak, size_t* count) {
   if (live) *live = g_live.load();
   if (peak) *peak = g_peak.load();
   if (count) *count = g_count.load();
+}
+
+size_t mpy_rt_mem_cached(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (device >= 0) return device < kMaxDevices ? g_pools[device].cached_bytes : 0;
+  size_t t = 0;
+  for (int d = 0; d < kMaxDevices; ++d) t += g_pools[d].cached_bytes;
+  return t;
 }
 
 int mpy_rt_fill_u32(void* ptr, uint32_t value, size_t nbytes, hipStream_t stream) {
