@@ -132,10 +132,15 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
         Vec<T, VEC> x[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<T, VEC>(tb + k + u * stepk);
+        // all UNROLL loads are issued before the first use (the scheduler would otherwise hoist
+        // arithmetic between them and wait on the first load early)
+        __builtin_amdgcn_sched_barrier(0);
+        T xs[UNROLL][VEC];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x[u].v[v], int64_t(k + u * stepk + v));
+          for (int v = 0; v < VEC; ++v) xs[u][v] = x[u].v[v];
+        acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk);
       }
       for (; k < n; k += stepk)
 #pragma unroll
@@ -201,10 +206,14 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
         Vec<T, VEC> x[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
+        for (int v = 0; v < VEC; ++v) {
+          T xs[UNROLL][1];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x[u].v[v], int64_t(k + u * kWaves - k0));
+          for (int u = 0; u < UNROLL; ++u) xs[u][0] = x[u].v[v];
+          acc[v] = Op::template step_chunk<UNROLL, 1>(acc[v], xs, uint32_t(k - k0), uint32_t(kWaves));
+        }
       }
       for (; k < k1; k += kWaves) {
         Vec<T, VEC> x = vload_nt<T, VEC>(base + int64_t(k) * ca.rs);
@@ -234,6 +243,68 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
       write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
     }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// wide col kernel: block = (outer, column group, tile) with all kRBlock lanes side by side over
+// kRBlock * VEC adjacent columns (4 KB of each row for f32), each lane walking the tile's rows
+// for its own VEC columns with UNROLL row loads in flight.  No cross-lane combine; every lane
+// writes its VEC results.
+template <class Op, class T, int VEC, int UNROLL, int WRITE>
+__global__ __launch_bounds__(kRBlock) void k_reduce_colw(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
+                                                         bool vec_ok) {
+  using A = typename Op::A;
+  const uint32_t b = blockIdx.x;
+  const uint32_t t = b % ca.tiles;
+  const uint32_t rest = b / ca.tiles;
+  const uint32_t cg = rest % ca.cgroups;
+  const uint32_t outer = rest / ca.cgroups;
+  const uint64_t c0 = (uint64_t(cg) * kRBlock + threadIdx.x) * VEC;
+  if (c0 >= ca.C) return;  // no barriers below
+  int64_t off[1];
+  row_offsets<1>(ca.ix, outer, off);
+  const T* base = a + off[0] + c0;
+  const uint64_t k0 = uint64_t(t) * ca.chunk;
+  const uint64_t k1 = k0 + ca.chunk < ca.R ? k0 + ca.chunk : ca.R;
+  const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;  // tile-relative indices below
+  const T* tb = base + int64_t(k0) * ca.rs;
+  A acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = Op::init();
+  if (vec_ok && c0 + VEC <= ca.C) {
+    uint32_t k = 0;
+    for (; k + UNROLL <= n; k += UNROLL) {
+      Vec<T, VEC> x[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<T, VEC>(tb + int64_t(k + u) * ca.rs);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        T xs[UNROLL][1];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) xs[u][0] = x[u].v[v];
+        acc[v] = Op::template step_chunk<UNROLL, 1>(acc[v], xs, k, 1);
+      }
+    }
+    for (; k < n; ++k) {
+      Vec<T, VEC> x = vload_nt<T, VEC>(tb + int64_t(k) * ca.rs);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k));
+    }
+  } else {
+    for (uint32_t k = 0; k < n; ++k)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (c0 + v < ca.C) acc[v] = Op::step(acc[v], tb[int64_t(k) * ca.rs + v], int64_t(k));
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    if (c0 + v >= ca.C) break;
+    A r = acc[v];
+    if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, base[v]);
+    const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
+    write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
   }
 }
 
@@ -366,6 +437,11 @@ void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, con
       k_reduce_row<Op, T, kRBlock, kWave, V, 2, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
     else
       k_reduce_row<Op, T, kRBlock, kWave, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
+  } else if (seg >= 8 && ra.rs == 1) {
+    // short contiguous segments (e.g. the [out][tiles] partials of a final): 16 lanes per
+    // output read one coalesced run instead of one lane striding through it
+    unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock / 16));
+    k_reduce_row<Op, T, kRBlock, 16, 1, 2, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);
   } else {
     unsigned grid = unsigned(ceil_div(ra.nwork, kRBlock));
     k_reduce_row<Op, T, kRBlock, 1, 1, 4, WRITE><<<grid, kRBlock, 0, st>>>(a, ra, out);

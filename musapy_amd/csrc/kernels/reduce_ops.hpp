@@ -59,6 +59,18 @@ template <> struct SumAcc<int64_t> { using A = uint64_t; };  // two's-complement
 template <> struct SumAcc<c64> { using A = c128; };
 template <> struct SumAcc<c128> { using A = c128; };
 
+// A chunk of U x V elements one lane loaded together: element (u, v) sits at tile-relative index
+// k + u * stepk + v, so (u, v) in lexicographic order is increasing index.  The default folds the
+// chunk element by element in that order.
+template <class Op, class A, class T, int U, int V>
+__device__ inline A fold_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc = Op::step(acc, x[u][v], int64_t(k + u * stepk + v));
+  return acc;
+}
+
 template <class T>
 struct OpSum {
   using A = typename SumAcc<T>::A;
@@ -67,6 +79,10 @@ struct OpSum {
   __device__ static A init() { return A(0); }
   __device__ static A step(A acc, T v, int64_t) { return acc + A(v); }
   __device__ static A comb(A a, A b) { return a + b; }
+  template <int U, int V>
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+    return fold_chunk<OpSum, A, T, U, V>(acc, x, k, stepk);
+  }
 };
 template <> __device__ inline c128 OpSum<c64>::init() { return c128{0.0, 0.0}; }
 template <> __device__ inline c128 OpSum<c64>::step(c128 acc, c64 v, int64_t) {
@@ -87,6 +103,10 @@ struct OpProd {
   __device__ static A init() { return A(1); }
   __device__ static A step(A acc, T v, int64_t) { return acc * A(v); }
   __device__ static A comb(A a, A b) { return a * b; }
+  template <int U, int V>
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+    return fold_chunk<OpProd, A, T, U, V>(acc, x, k, stepk);
+  }
 };
 __device__ inline c128 cmul(c128 a, c128 b) {
   return c128{a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
@@ -128,6 +148,40 @@ struct OpExt {
   __device__ static A step_pair(A acc, T v, int64_t k) {
     if (k < 0 || is_nan(v)) return acc;
     return comb(acc, A{v, I(k)});
+  }
+  // Two phases per chunk: m = the chunk's extreme over its non-NaN elements (fmax/fmin drop a
+  // NaN operand), then, only when m beats the running result, the first element equal to m.
+  // That element is the one the sequential scan keeps: every earlier element is smaller (or
+  // NaN), and equality also matches +0 against -0, so the kept bits are the first zero's.  A tie
+  // with the running result keeps the running (lower) index.
+  template <int U, int V>
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+    T m = x[0][0];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = (u == 0 ? 1 : 0); v < V; ++v) m = pick(m, x[u][v]);
+    const bool improve = acc.idx < 0 ? !is_nan(m) : better(m, acc.val);
+    if (improve) {
+      uint32_t off = 0;
+      T val = m;
+#pragma unroll
+      for (int u = U - 1; u >= 0; --u)
+#pragma unroll
+        for (int v = V - 1; v >= 0; --v)
+          if (x[u][v] == m) {
+            off = u * stepk + v;
+            val = x[u][v];
+          }
+      acc = A{val, I(k + off)};
+    }
+    return acc;
+  }
+  // the extreme of two values, ignoring a NaN operand (for integers: plain max/min)
+  __device__ static T pick(T a, T b) {
+    if constexpr (sizeof(T) == 4 && T(0.5) != T(0)) return MAX ? __builtin_fmaxf(a, b) : __builtin_fminf(a, b);
+    else if constexpr (sizeof(T) == 8 && T(0.5) != T(0)) return MAX ? __builtin_fmax(a, b) : __builtin_fmin(a, b);
+    else return MAX ? (b > a ? b : a) : (b < a ? b : a);
   }
 };
 

@@ -231,3 +231,11 @@ def test_cumsum_deterministic():
     s = ms.sum(X, axis=1).numpy()
     for _ in range(3):
         assert_bits_equal(ms.sum(X, axis=1).numpy(), s, "sum run-to-run")
+    # many rows: the block-per-row scan (no look-back)
+    y = RNG.random((600, 40000))
+    Y = dev(y)
+    b = ms.cumsum(Y, axis=1).numpy()
+    for _ in range(2):
+        assert_bits_equal(ms.cumsum(Y, axis=1).numpy(), b, "row-per-block cumsum run-to-run")
+    want = R.cumsum(y[:4], 1)
+    assert np.all(np.abs(b[:4] - want) <= 1e-12 * np.abs(want))
