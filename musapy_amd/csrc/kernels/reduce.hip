@@ -14,6 +14,7 @@
 // fixed, so results are identical from run to run.
 #include "kcommon.hpp"
 #include "reduce_ops.hpp"
+#include "publish.hpp"
 #include "../../../include/musapy_kernels.h"
 
 namespace mpy {
@@ -106,6 +107,52 @@ struct RowArgs {
   bool nt;            // streaming loads (launch input volume >= kStreamLoadBytes)
 };
 
+// One lane's share of a segment: lane l of a GROUP-lane group reduces elements l*VEC, l*VEC +
+// GROUP*VEC, ... of the n-element segment at tb (indices relative to tb).
+template <class Op, class T, int GROUP, int VEC, int UNROLL>
+__device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, uint32_t n, int l, int64_t rs,
+                                                    bool nt) {
+  using A = typename Op::A;
+  A acc = Op::init();
+  uint32_t k = uint32_t(l) * VEC;
+  constexpr uint32_t stepk = uint32_t(GROUP) * VEC;
+  if (VEC > 1) {
+    for (; k + (UNROLL - 1) * stepk + VEC <= n; k += UNROLL * stepk) {
+      Vec<T, VEC> x[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) x[u] = vload_pol<T, VEC>(tb + k + u * stepk, nt);
+      // all UNROLL loads are issued before the first use (the scheduler would otherwise hoist
+      // arithmetic between them and wait on the first load early)
+      __builtin_amdgcn_sched_barrier(0);
+      T xs[UNROLL][VEC];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) xs[u][v] = x[u].v[v];
+      acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk);
+    }
+    for (; k + VEC <= n; k += stepk) {  // whole vectors left
+      Vec<T, VEC> x = vload_pol<T, VEC>(tb + k, nt);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x.v[v], int64_t(k + v));
+    }
+    if (k < n)  // the last, partial vector of the tile
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (k + v < n) acc = Op::step(acc, tb[k + v], int64_t(k + v));
+  } else {
+    for (; k + (UNROLL - 1) * stepk < n; k += UNROLL * stepk) {
+      T x[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) x[u] = tb[int64_t(k + u * stepk) * rs];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
+    }
+    for (; k < n; k += stepk) acc = Op::step(acc, tb[int64_t(k) * rs], int64_t(k));
+  }
+  return acc;
+}
+
 template <class Op, class T, int BS, int GROUP, int VEC, int UNROLL, int WRITE>
 __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowArgs ra, RedOut<T> out) {
   using A = typename Op::A;
@@ -126,48 +173,124 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
     const uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
     const T* tb = base + int64_t(k0) * ra.rs;  // indices below are relative to the tile start
     const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;
-    uint32_t k = uint32_t(l) * VEC;
-    constexpr uint32_t stepk = uint32_t(GROUP) * VEC;
-    if (VEC > 1) {
-      for (; k + (UNROLL - 1) * stepk + VEC <= n; k += UNROLL * stepk) {
-        Vec<T, VEC> x[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = vload_pol<T, VEC>(tb + k + u * stepk, ra.nt);
-        // all UNROLL loads are issued before the first use (the scheduler would otherwise hoist
-        // arithmetic between them and wait on the first load early)
-        __builtin_amdgcn_sched_barrier(0);
-        T xs[UNROLL][VEC];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) xs[u][v] = x[u].v[v];
-        acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk);
-      }
-      for (; k + VEC <= n; k += stepk) {  // whole vectors left
-        Vec<T, VEC> x = vload_pol<T, VEC>(tb + k, ra.nt);
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x.v[v], int64_t(k + v));
-      }
-      if (k < n)  // the last, partial vector of the tile
-#pragma unroll
-        for (int v = 0; v < VEC; ++v)
-          if (k + v < n) acc = Op::step(acc, tb[k + v], int64_t(k + v));
-    } else {
-      const int64_t rs = ra.rs;
-      for (; k + (UNROLL - 1) * stepk < n; k += UNROLL * stepk) {
-        T x[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = tb[int64_t(k + u * stepk) * rs];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
-      }
-      for (; k < n; k += stepk) acc = Op::step(acc, tb[int64_t(k) * rs], int64_t(k));
-    }
+    acc = accumulate_segment<Op, T, GROUP, VEC, UNROLL>(tb, n, l, ra.rs, ra.nt);
   }
   acc = group_reduce<Op, GROUP>(acc);
   if (live && (GROUP <= kWave ? l == 0 : threadIdx.x == 0)) {
     if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
     write_result<Op, T, WRITE>(out, w, acc, int64_t(k0));
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// Fused partial + final for few outputs.  Blocks 0 .. out_size*tiles-1 are the row kernel's
+// (output, tile) blocks; each publishes its tile's accumulator (publish.hpp) and exits.  Blocks
+// out_size*tiles + o, the last of the grid, are combiners: the dispatcher hands them out after
+// every streaming block, so they poll the slots while the last tiles are still streaming and
+// finish right after the last publish.  Lane l of a combiner owns tiles l, l + 512, ... (at most
+// kFusedPerLane), waits until all of them are published (a bounded poll), folds them in ascending
+// order, and the block tree combines the lanes: a fixed order, independent of timing.  A combiner
+// holds one block slot; with at most kFusedMaxOutputs of them the streaming blocks always find
+// room, so the waits end.  Every slot read is cleared again, leaving the workspace zero.
+// Workspace: out_size * tiles * W slot words.
+constexpr int kFusedPerLane = 8;
+constexpr size_t kFusedMaxOutputs = 64;
+constexpr size_t kFusedMaxTiles = 2048;  // <= kFusedPerLane * kRowBS
+struct FusedArgs {
+  uint64_t* slots;
+  uint32_t spin_limit;
+};
+
+// a tile's accumulator (tile-relative int32 index) as the final's accumulator (absolute index)
+template <class Op, class OpF>
+__device__ inline typename OpF::A to_final(const typename Op::A& x, int64_t k0) {
+  if constexpr (Op::kOrdered) {
+    return typename OpF::A{x.val, x.idx < 0 ? int64_t(-1) : k0 + int64_t(x.idx)};
+  } else {
+    return x;
+  }
+}
+
+template <class Op, class OpF, class T, int VEC, int UNROLL>
+__global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict__ a, RowArgs ra, RedOut<T> out,
+                                                             FusedArgs fa) {
+  using A = typename Op::A;
+  using AF = typename OpF::A;
+  static_assert(sizeof(A) % 4 == 0, "accumulator must split into 32-bit slices");
+  constexpr int W = int(sizeof(A) / 4);
+  const uint64_t w = blockIdx.x;
+  if (w < ra.nwork) {  // a streaming (output, tile) block
+    const uint64_t o = w / ra.tiles;
+    const uint64_t t = w - o * ra.tiles;
+    int64_t off[1];
+    row_offsets<1>(ra.ix, uint32_t(o), off);
+    const T* base = a + off[0];
+    const uint64_t k0 = t * ra.chunk;
+    const uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
+    const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;
+    A acc =
+        accumulate_segment<Op, T, kRowBS, VEC, UNROLL>(base + int64_t(k0) * ra.rs, n, threadIdx.x, ra.rs, ra.nt);
+    acc = group_reduce<Op, kRowBS>(acc);
+    if (threadIdx.x == 0) {
+      if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
+      uint32_t s[W];
+      __builtin_memcpy(s, &acc, sizeof(A));
+      publish_slices<W>(fa.slots + w * W, s);
+    }
+    return;
+  }
+  // combiner of output o
+  const uint64_t o = w - ra.nwork;
+  uint64_t* row_slots = fa.slots + o * ra.tiles * W;
+  uint64_t v[kFusedPerLane][W] = {};
+  uint32_t pending = 0;
+#pragma unroll
+  for (int j = 0; j < kFusedPerLane; ++j)
+    if (threadIdx.x + j * kRowBS < ra.tiles) pending |= 1u << j;
+  for (uint32_t spins = 0; pending != 0 && spins < fa.spin_limit; ++spins) {
+    uint64_t u[kFusedPerLane][W];
+#pragma unroll
+    for (int j = 0; j < kFusedPerLane; ++j)  // every outstanding slot's words in flight together
+      if (pending & (1u << j))
+#pragma unroll
+        for (int i = 0; i < W; ++i) u[j][i] = ld_relaxed(row_slots + uint64_t(threadIdx.x + j * kRowBS) * W + i);
+#pragma unroll
+    for (int j = 0; j < kFusedPerLane; ++j) {
+      if (!(pending & (1u << j))) continue;
+      bool ready = true;
+#pragma unroll
+      for (int i = 0; i < W; ++i) ready = ready && (u[j][i] & kTag);
+      if (ready) {
+#pragma unroll
+        for (int i = 0; i < W; ++i) v[j][i] = u[j][i];
+        pending &= ~(1u << j);
+      }
+    }
+    if (pending) __builtin_amdgcn_s_sleep(2);
+  }
+  AF r = OpF::init();
+  A first{};
+#pragma unroll
+  for (int j = 0; j < kFusedPerLane; ++j) {
+    const uint32_t tt = threadIdx.x + j * kRowBS;
+    if (tt >= ra.tiles) break;
+    uint32_t s[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) s[i] = uint32_t(v[j][i]);
+    A x;
+    __builtin_memcpy(&x, s, sizeof(A));
+    if (tt == 0) first = x;
+    r = OpF::comb(r, to_final<Op, OpF>(x, int64_t(tt) * int64_t(ra.chunk)));
+#pragma unroll
+    for (int i = 0; i < W; ++i) st_relaxed(row_slots + uint64_t(tt) * W + i, 0);
+  }
+  r = group_reduce<OpF, kRowBS>(r);
+  if (threadIdx.x == 0) {
+    if constexpr (Op::kOrdered) {
+      // a NaN at axis position 0 absorbed tile 0 and therefore the whole reduction
+      if (first.idx >= 0 && is_nan(first.val)) r = to_final<Op, OpF>(first, 0);
+    }
+    write_result<OpF, T, kWriteFinal>(out, o, r, 0);
   }
 }
 
@@ -511,6 +634,41 @@ template <class T> inline RedOut<T> vout(T* c) { return RedOut<T>{c, nullptr, 0.
 template <class T> inline RedOut<T> iout(int64_t* c) { return RedOut<T>{nullptr, c, 0.0, kFinPlain}; }
 template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c, nullptr, cnt, kFinMean}; }
 
+// the fused single launch for a row-kind reduction split into `tiles` tiles; false (nothing
+// launched) when the shape does not take the 512-lane block path or the workspace is too small
+template <class Op, class OpF, class T>
+bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                         size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (out_size == 0 || out_size > kFusedMaxOutputs || axis_len == 0 || tiles < 2 || ws == nullptr) return false;
+  // a combiner lane folds at most kFusedPerLane tiles; 2048 tiles measured best for 64M f32
+  if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
+  ReducePlan p;
+  plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
+  if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return false;
+  for (int d = 0; d < p.ond; ++d)
+    if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return false;
+  constexpr int V = rvec<T>();
+  uint64_t chunk = ceil_div(ceil_div(p.R, tiles), uint64_t(V)) * V;
+  if (chunk * sizeof(T) < 16384 || chunk >= (uint64_t(1) << 31)) return false;
+  const uint64_t W = sizeof(typename Op::A) / 4;
+  const uint64_t words = uint64_t(out_size) * tiles * W;
+  if (words * 8 > ws_bytes || uint64_t(out_size) * tiles >= (uint64_t(1) << 31)) return false;
+  RowArgs ra{};
+  ra.nt = true;
+  ra.ix = out_indexer(p, p.ond);
+  ra.R = p.R;
+  ra.rs = 1;
+  ra.tiles = uint32_t(tiles);
+  ra.chunk = chunk;
+  ra.nwork = uint64_t(out_size) * tiles;
+  FusedArgs fa{};
+  fa.slots = static_cast<uint64_t*>(ws);
+  fa.spin_limit = 1u << 24;
+  // streaming blocks first, then one combiner per output
+  k_reduce_row_fused<Op, OpF, T, V, 4><<<dim3(unsigned(ra.nwork + out_size)), kRowBS, 0, st>>>(a, ra, out, fa);
+  return true;
+}
+
 }  // namespace mpy
 
 
@@ -642,5 +800,57 @@ MPY_RED_ARG(argmax, OpArgmax, f64, double)
 MPY_RED_ARG(argmin, OpArgmin, i64, int64_t)
 MPY_RED_ARG(argmin, OpArgmin, f32, float)
 MPY_RED_ARG(argmin, OpArgmin, f64, double)
+
+// partial + final in one launch (new; see musapy_kernels.h)
+int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
+                           const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles,
+                           void* workspace, size_t workspace_bytes, hipStream_t st) {
+#define FUSED_CASE(T)                                                                                           \
+  {                                                                                                             \
+    const T* x = static_cast<const T*>(a);                                                                      \
+    T* cv = static_cast<T*>(c);                                                                                 \
+    int64_t* ci = static_cast<int64_t*>(c);                                                                     \
+    bool ok = false;                                                                                            \
+    switch (op) {                                                                                               \
+      case MUSAPY_RED_SUM:                                                                                      \
+        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,             \
+                                                        workspace_bytes, st);                                   \
+        break;                                                                                                  \
+      case MUSAPY_RED_PROD:                                                                                     \
+        ok = launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,           \
+                                                          workspace_bytes, st);                                 \
+        break;                                                                                                  \
+      case MUSAPY_RED_MAX:                                                                                      \
+        ok = launch_reduce_fused<OpMax<T>, OpExt<T, true, false, int64_t>, T>(x, vout<T>(cv), RED_PASS, tiles,  \
+                                                                              workspace, workspace_bytes, st);  \
+        break;                                                                                                  \
+      case MUSAPY_RED_MIN:                                                                                      \
+        ok = launch_reduce_fused<OpMin<T>, OpExt<T, false, false, int64_t>, T>(x, vout<T>(cv), RED_PASS, tiles, \
+                                                                               workspace, workspace_bytes, st); \
+        break;                                                                                                  \
+      case MUSAPY_RED_MEAN:                                                                                     \
+        if (sizeof(T) == 8 && T(0.5) == T(0)) break; /* integer means go through f64 */                         \
+        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, mean_count<T>(axis_len)), RED_PASS,      \
+                                                        tiles, workspace, workspace_bytes, st);                 \
+        break;                                                                                                  \
+      case MUSAPY_RED_ARGMAX:                                                                                   \
+        ok = launch_reduce_fused<OpArgmax<T>, OpArgmax64<T>, T>(x, iout<T>(ci), RED_PASS, tiles, workspace,     \
+                                                                workspace_bytes, st);                           \
+        break;                                                                                                  \
+      case MUSAPY_RED_ARGMIN:                                                                                   \
+        ok = launch_reduce_fused<OpArgmin<T>, OpArgmin64<T>, T>(x, iout<T>(ci), RED_PASS, tiles, workspace,     \
+                                                                workspace_bytes, st);                           \
+        break;                                                                                                  \
+    }                                                                                                           \
+    return ok ? 0 : -1;                                                                                         \
+  }
+  switch (dtype) {
+    case MUSAPY_DT_F32: FUSED_CASE(float)
+    case MUSAPY_DT_F64: FUSED_CASE(double)
+    case MUSAPY_DT_I64: FUSED_CASE(int64_t)
+  }
+#undef FUSED_CASE
+  return -1;
+}
 
 }  // extern "C"

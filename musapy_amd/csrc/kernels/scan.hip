@@ -16,6 +16,7 @@
 //   generic  one lane per row, sequential along the axis (any strides).
 // col and generic add in exactly the reference CPU order (acc = 0; acc += x[k]).
 #include "kcommon.hpp"
+#include "publish.hpp"
 #include "../../../include/musapy_kernels.h"
 
 namespace mpy {
@@ -41,36 +42,8 @@ template <> __device__ inline double from_bits<double>(uint64_t b) { return __lo
 template <> __device__ inline float from_bits<float>(uint64_t b) { return __uint_as_float(uint32_t(b)); }
 template <> __device__ inline uint64_t from_bits<uint64_t>(uint64_t b) { return b; }
 
-// Published look-back values.  Agent-scope acquire/release would make every publish write back
-// and every poll invalidate a whole L2 on this multi-XCD part, so there are no fences at all:
-// a value is stored as W 64-bit words, each holding a 32-bit slice of its bits next to a
-// "published" tag, with relaxed (but coherent) 64-bit atomics.  Each word is written once per
-// launch, so a reader that sees the tag on every word holds the final value.
-__device__ inline uint64_t ld_relaxed(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void st_relaxed(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-constexpr uint64_t kTag = uint64_t(1) << 32;
-
-template <int W>
-__device__ inline void publish_value(uint64_t* w, uint64_t bits) {
-  st_relaxed(w, kTag | (bits & 0xffffffffu));
-  if (W == 2) st_relaxed(w + 1, kTag | (bits >> 32));
-}
-template <int W>
-__device__ inline bool read_value(const uint64_t* w, uint64_t& bits) {
-  uint64_t lo = ld_relaxed(w);
-  if (!(lo & kTag)) return false;
-  uint64_t hi = 0;
-  if (W == 2) {
-    hi = ld_relaxed(w + 1);
-    if (!(hi & kTag)) return false;
-  }
-  bits = (lo & 0xffffffffu) | ((hi & 0xffffffffu) << 32);
-  return true;
-}
+// Published look-back values (publish.hpp): each status word is written once per launch after
+// k_scan_clear zeroed it, so a reader that sees the tag on every word holds the final value.
 
 __global__ void k_scan_clear(uint64_t* w, uint64_t n) {
   for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x)

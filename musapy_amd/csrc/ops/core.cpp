@@ -225,7 +225,22 @@ Stream::Stream(int device, hipStream_t raw, bool owned)
     : device_(device), raw_(raw), owned_(owned), id_(g_stream_ids.fetch_add(1)) {}
 
 Stream::~Stream() {
+  if (workspace_) mpy_rt_free(workspace_, raw_);
   if (owned_ && raw_) mpy_rt_stream_destroy(raw_);
+}
+
+void* Stream::reduce_workspace() {
+  if (!workspace_) {
+    void* p = nullptr;
+    check_rt(mpy_rt_malloc(&p, kReduceWorkspaceBytes, device_, raw_), "reduction workspace");
+    int code = mpy_rt_fill_u32(p, 0u, kReduceWorkspaceBytes, raw_);
+    if (code != 0) {
+      mpy_rt_free(p, raw_);
+      check_rt(code, "reduction workspace clear");
+    }
+    workspace_ = p;
+  }
+  return workspace_;
 }
 
 void Stream::synchronize() {

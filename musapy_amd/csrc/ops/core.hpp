@@ -87,6 +87,11 @@ class Stream {
   // synchronize; a failure poisons the stream and raises StreamError (stream.rs:311-377)
   void synchronize();
   static std::shared_ptr<Stream> create(int device);
+  // Scratch for the single-launch reductions queued on this stream: zero-filled once when first
+  // requested, and every such launch leaves it zero again.  Work on one stream is ordered, so
+  // its launches never share it concurrently.
+  static constexpr size_t kReduceWorkspaceBytes = size_t(1) << 20;
+  void* reduce_workspace();
 
  private:
   int device_;
@@ -94,6 +99,7 @@ class Stream {
   bool owned_;
   bool poisoned_ = false;
   uint64_t id_;
+  void* workspace_ = nullptr;
 };
 using StreamPtr = std::shared_ptr<Stream>;
 

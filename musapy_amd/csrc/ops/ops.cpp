@@ -430,6 +430,31 @@ void red_single(ReduceKernel k, Dtype ct, const RedCall& c, void* out) {
 #undef R1
 }
 
+// partial + final in one launch (musapy_reduce_fused_v1) with the stream's workspace; false when
+// the kernel library does not cover the case (then the two-stage path runs)
+bool red_fused(ReduceKernel k, Dtype ct, const RedCall& c, void* out, size_t tiles, Stream& s) {
+  int op = 0;
+  switch (k) {
+    case ReduceKernel::Sum: op = MUSAPY_RED_SUM; break;
+    case ReduceKernel::Prod: op = MUSAPY_RED_PROD; break;
+    case ReduceKernel::Max: op = MUSAPY_RED_MAX; break;
+    case ReduceKernel::Min: op = MUSAPY_RED_MIN; break;
+    case ReduceKernel::Mean: op = MUSAPY_RED_MEAN; break;
+    case ReduceKernel::Argmax: op = MUSAPY_RED_ARGMAX; break;
+    case ReduceKernel::Argmin: op = MUSAPY_RED_ARGMIN; break;
+    default: return false;
+  }
+  int dt = 0;
+  switch (ct) {
+    case Dtype::Float32: dt = MUSAPY_DT_F32; break;
+    case Dtype::Float64: dt = MUSAPY_DT_F64; break;
+    case Dtype::Int64: dt = MUSAPY_DT_I64; break;
+    default: return false;
+  }
+  return musapy_reduce_fused_v1(op, dt, c.a, out, c.nd, c.shape, c.strides, c.axis, c.axis_len, c.out_size, tiles,
+                                s.reduce_workspace(), Stream::kReduceWorkspaceBytes, c.s) == 0;
+}
+
 // partial -> final for value reductions (sum/prod/max/min/mean)
 void red_two_stage(ReduceKernel k, Dtype ct, const RedCall& c, void* out, size_t tiles, void* partials) {
 #define P2(OP, SFX, T) musapy_##OP##_partial_##SFX##_v2((const T*)c.a, (T*)partials, RED_CALL_ARGS, tiles, c.s)
@@ -557,6 +582,8 @@ Array reduction_axis(const Array& a, std::optional<size_t> axis, bool keepdims, 
                                  : musapy_reduce_tiles_hint(c.nd, c.shape, c.strides, c.axis, axis_len, out_size, es);
     if (tiles <= 1) {
       red_single(k, ct, c, r.data_ptr());
+    } else if (red_fused(k, ct, c, r.data_ptr(), tiles, *s)) {
+      // one launch: partials handed over through the stream's workspace
     } else if (is_arg(k)) {
       BufferRef pv = Buffer::alloc(out_size * tiles * es, a.device, s);
       BufferRef pi = Buffer::alloc(out_size * tiles * 8, a.device, s);

@@ -144,6 +144,43 @@ def test_multi_axis_merged(kind, dt):
         check_reduce(kind, xt, axes, gpu_x=gx)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_single_launch_tiled_reductions(dt):
+    """Reductions large enough to be split into tiles (> 256 KB with few outputs) run as one
+    launch that hands tile results over through the stream's workspace; the workspace must be
+    left clean, so the cases run back to back with changing shapes and repeats."""
+    n = 3_000_001
+    if dt == np.int64:
+        x = RNG.integers(-(2**40), 2**40, n).astype(np.int64)
+    else:
+        x = RNG.standard_normal(n).astype(dt)
+    X = dev(x)
+    for kind in ("sum", "max", "min", "argmax", "argmin", "mean", "sum"):
+        if kind == "mean" and dt == np.int64:
+            continue
+        check_reduce(kind, x, None, gpu_x=X)
+    m = x[: 7 * 400_000].reshape(7, 400_000)  # few outputs, several tiles each
+    M = dev(m)
+    for kind in ("argmax", "sum", "min", "argmin"):
+        check_reduce(kind, m, 1, gpu_x=M)
+        check_reduce(kind, m, 1, gpu_x=M)
+    if dt != np.int64:
+        # NaN at position 0 absorbs; a NaN elsewhere is skipped; ties go to the lowest index
+        y = x.copy()
+        y[0] = np.nan
+        for kind in ("max", "argmax", "min", "argmin"):
+            check_reduce(kind, y, None)
+        z = x.copy()
+        z[1_234_567] = np.nan
+        z[2_500_000] = z[2_900_000] = np.abs(z).max() + 1
+        for kind in ("max", "argmax"):
+            check_reduce(kind, z, None)
+    t = np.zeros(2_000_000, dt)
+    t[[5, 1_999_999]] = 3
+    for kind in ("argmax", "argmin"):
+        check_reduce(kind, t, None)
+
+
 @pytest.mark.parametrize("dt", [np.complex64, np.complex128])
 def test_complex_reductions(dt):
     for shape, axes in (((3, 4), [None, 0, 1, (0, 1), -1]), ((16, 64, 64), [(1, 2), 0, 2]), ((4, 200000), [1])):
