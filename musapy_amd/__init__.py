@@ -27,12 +27,14 @@ from ._core import (  # noqa: F401
     sum, prod, max, min, mean, argmax, argmin, cumsum,
     transpose, flip, index_select, contiguous,
     set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats, empty_cache,
+    Stream, stream, current_stream,
 )
 
 __all__ = [
     "Array", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp", "log",
     "abs", "sign", "neg", "clamp", "astype", "sum", "prod", "max", "min", "mean", "argmax", "argmin",
-    "cumsum", "transpose", "permute", "flip", "slice", "index_select", "contiguous",
+    "cumsum", "transpose", "permute", "flip", "slice", "index_select", "contiguous", "Stream", "stream",
+    "current_stream", "synchronize",
 ]
 
 # dtype names (musapy exposes ms.float32 etc. as dtype objects; here they are the dtype strings)

@@ -353,7 +353,9 @@ Array new_array(const Shape& shape, Dtype dtype, int device, const StreamPtr& st
 }
 
 Array from_host(const void* src, const Shape& shape, Dtype dtype, int device) {
-  StreamPtr s = default_stream(device);
+  // inside a stream context on this device the array belongs to that stream (resolution.rs)
+  StreamPtr cur = current_stream();
+  StreamPtr s = cur && cur->device() == device ? cur : default_stream(device);
   Array a = new_array(shape, dtype, device, s);
   size_t n = shape_numel(shape) * element_size(dtype);
   if (n) check_rt(mpy_rt_memcpy_h2d(a.data->ptr(), src, n, s->raw()), "host-to-device copy");

@@ -87,6 +87,10 @@ class Stream {
   // synchronize; a failure poisons the stream and raises StreamError (stream.rs:311-377)
   void synchronize();
   static std::shared_ptr<Stream> create(int device);
+  // The priority a caller asked for (stream.rs:154-199).  It is recorded, not applied: every
+  // stream of this backend runs at the default priority.
+  int priority() const { return priority_; }
+  void set_priority(int p) { priority_ = p; }
   // Scratch for the single-launch reductions queued on this stream: zero-filled once when first
   // requested, and every such launch leaves it zero again.  Work on one stream is ordered, so
   // its launches never share it concurrently.
@@ -99,6 +103,7 @@ class Stream {
   bool owned_;
   bool poisoned_ = false;
   uint64_t id_;
+  int priority_ = 0;
   void* workspace_ = nullptr;
 };
 using StreamPtr = std::shared_ptr<Stream>;

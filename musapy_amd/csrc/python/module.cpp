@@ -138,7 +138,49 @@ PYBIND11_MODULE(_core, m) {
   py::register_exception<StreamError>(m, "StreamError", base.ptr());
   py::register_exception<KernelError>(m, "KernelError", base.ptr());
 
+  // streams (rust/musapy-python/src/stream.rs:14-80; lib.rs:57-70, 126-130)
+  py::class_<Stream, StreamPtr>(m, "Stream")
+      .def(py::init([](py::object device, int priority) {
+             StreamPtr s = Stream::create(parse_device(device));
+             s->set_priority(priority);
+             return s;
+           }),
+           py::arg("device") = py::none(), py::arg("priority") = 0)
+      .def("synchronize", [](Stream& s) {
+        py::gil_scoped_release nogil;
+        s.synchronize();
+      })
+      .def_property_readonly("priority", &Stream::priority)
+      .def_property_readonly("device", [](const Stream& s) { return dev_str(s.device()); })
+      .def_property_readonly("id", &Stream::id)
+      .def_property_readonly("is_poisoned", &Stream::is_poisoned)
+      .def("__eq__", [](const Stream& a, const Stream& b) { return &a == &b; })
+      .def("__hash__", [](const Stream& s) { return s.id(); })
+      .def("__repr__", [](const Stream& s) {
+        return "Stream(device=" + dev_str(s.device()) + ", id=" + std::to_string(s.id()) + ")";
+      });
+  struct StreamContext {
+    StreamPtr s, prev;
+  };
+  py::class_<StreamContext>(m, "_StreamContext")
+      .def("__enter__", [](StreamContext& c) {
+        c.prev = current_stream();
+        set_current_stream(c.s);
+        return c.s;
+      })
+      .def("__exit__", [](StreamContext& c, py::object, py::object, py::object) {
+        set_current_stream(c.prev);
+        c.prev.reset();
+      });
+  m.def("stream", [](StreamPtr s) { return StreamContext{std::move(s), nullptr}; }, py::arg("stream"));
+  m.def("current_stream", []() -> py::object {
+    StreamPtr s = current_stream();
+    if (s) return py::cast(s);
+    return py::cast(default_stream(g_default_device));
+  });
+
   py::class_<Array>(m, "Array")
+      .def_property_readonly("stream", [](const Array& a) { return a.stream; })
       .def_property_readonly("shape", [](const Array& a) { return to_tuple(a.shape()); })
       .def_property_readonly("ndim", [](const Array& a) { return a.ndim(); })
       .def_property_readonly("size", [](const Array& a) { return a.size(); })
@@ -233,6 +275,8 @@ PYBIND11_MODULE(_core, m) {
     int dv = parse_device(d);
     py::gil_scoped_release nogil;
     default_stream(dv)->synchronize();
+    check_rt(mpy_rt_set_device(dv), "set device");
+    check_rt(mpy_rt_device_synchronize(), "device synchronize");  // user streams too
   }, py::arg("device") = py::none());
   m.def("device_count", []() {
     int n = 0;
