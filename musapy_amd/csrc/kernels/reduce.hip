@@ -108,14 +108,17 @@ struct RowArgs {
 };
 
 // One lane's share of a segment: lane l of a GROUP-lane group reduces elements l*VEC, l*VEC +
-// GROUP*VEC, ... of the n-element segment at tb (indices relative to tb).
+// GROUP*VEC, ... of the n-element segment at tb (indices relative to tb).  Lane 0 also returns
+// the segment's first element in `first` (ordered reductions need it for the NaN-at-0 rule; it
+// is kept from the load instead of being read again at the end).
 template <class Op, class T, int GROUP, int VEC, int UNROLL>
 __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, uint32_t n, int l, int64_t rs,
-                                                    bool nt) {
+                                                    bool nt, T& first) {
   using A = typename Op::A;
   A acc = Op::init();
   uint32_t k = uint32_t(l) * VEC;
   constexpr uint32_t stepk = uint32_t(GROUP) * VEC;
+  const bool lead = l == 0;  // lane 0 starts at element 0
   if (VEC > 1) {
     for (; k + (UNROLL - 1) * stepk + VEC <= n; k += UNROLL * stepk) {
       Vec<T, VEC> x[UNROLL];
@@ -129,26 +132,38 @@ __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, ui
       for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
         for (int v = 0; v < VEC; ++v) xs[u][v] = x[u].v[v];
+      if (Op::kOrdered && lead && k == 0) first = xs[0][0];
       acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk);
     }
     for (; k + VEC <= n; k += stepk) {  // whole vectors left
       Vec<T, VEC> x = vload_pol<T, VEC>(tb + k, nt);
+      if (Op::kOrdered && lead && k == 0) first = x.v[0];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x.v[v], int64_t(k + v));
     }
-    if (k < n)  // the last, partial vector of the tile
+    if (k < n) {  // the last, partial vector of the tile
 #pragma unroll
       for (int v = 0; v < VEC; ++v)
-        if (k + v < n) acc = Op::step(acc, tb[k + v], int64_t(k + v));
+        if (k + v < n) {
+          const T x = tb[k + v];
+          if (Op::kOrdered && lead && k + v == 0) first = x;
+          acc = Op::step(acc, x, int64_t(k + v));
+        }
+    }
   } else {
     for (; k + (UNROLL - 1) * stepk < n; k += UNROLL * stepk) {
       T x[UNROLL];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) x[u] = tb[int64_t(k + u * stepk) * rs];
+      if (Op::kOrdered && lead && k == 0) first = x[0];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
     }
-    for (; k < n; k += stepk) acc = Op::step(acc, tb[int64_t(k) * rs], int64_t(k));
+    for (; k < n; k += stepk) {
+      const T x = tb[int64_t(k) * rs];
+      if (Op::kOrdered && lead && k == 0) first = x;
+      acc = Op::step(acc, x, int64_t(k));
+    }
   }
   return acc;
 }
@@ -162,22 +177,21 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
   const bool live = w < ra.nwork;
   A acc = Op::init();
   uint64_t o = 0, t = 0, k0 = 0;
-  const T* base = a;
+  T first{};
   if (live) {
     o = w / ra.tiles;
     t = w - o * ra.tiles;
     int64_t off[1];
     row_offsets<1>(ra.ix, uint32_t(o), off);
-    base = a + off[0];
     k0 = t * ra.chunk;
     const uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
-    const T* tb = base + int64_t(k0) * ra.rs;  // indices below are relative to the tile start
+    const T* tb = a + off[0] + int64_t(k0) * ra.rs;  // indices below are relative to the tile start
     const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;
-    acc = accumulate_segment<Op, T, GROUP, VEC, UNROLL>(tb, n, l, ra.rs, ra.nt);
+    acc = accumulate_segment<Op, T, GROUP, VEC, UNROLL>(tb, n, l, ra.rs, ra.nt, first);
   }
   acc = group_reduce<Op, GROUP>(acc);
   if (live && (GROUP <= kWave ? l == 0 : threadIdx.x == 0)) {
-    if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
+    if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, first);
     write_result<Op, T, WRITE>(out, w, acc, int64_t(k0));
   }
 }
@@ -224,15 +238,15 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
     const uint64_t t = w - o * ra.tiles;
     int64_t off[1];
     row_offsets<1>(ra.ix, uint32_t(o), off);
-    const T* base = a + off[0];
     const uint64_t k0 = t * ra.chunk;
     const uint64_t k1 = k0 + ra.chunk < ra.R ? k0 + ra.chunk : ra.R;
     const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;
-    A acc =
-        accumulate_segment<Op, T, kRowBS, VEC, UNROLL>(base + int64_t(k0) * ra.rs, n, threadIdx.x, ra.rs, ra.nt);
+    T first{};
+    A acc = accumulate_segment<Op, T, kRowBS, VEC, UNROLL>(a + off[0] + int64_t(k0) * ra.rs, n, threadIdx.x, ra.rs,
+                                                           ra.nt, first);
     acc = group_reduce<Op, kRowBS>(acc);
     if (threadIdx.x == 0) {
-      if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, base[0]);
+      if (t == 0 && ra.R > 0) acc = absorb_first<Op, T>(acc, first);
       uint32_t s[W];
       __builtin_memcpy(s, &acc, sizeof(A));
       publish_slices<W>(fa.slots + w * W, s);
@@ -327,6 +341,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
   const uint64_t k0 = uint64_t(t) * ca.chunk;
   const uint64_t k1 = k0 + ca.chunk < ca.R ? k0 + ca.chunk : ca.R;
   A acc[VEC];
+  T first[VEC] = {};  // row 0 of the axis, kept by wave 0 for the NaN-at-0 rule
 #pragma unroll
   for (int v = 0; v < VEC; ++v) acc[v] = Op::init();
   if (c0 < ca.C) {
@@ -337,6 +352,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) x[u] = vload_pol<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs, ca.nt);
         __builtin_amdgcn_sched_barrier(0);
+        if (Op::kOrdered && k == 0)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) first[v] = x[0].v[v];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           T xs[UNROLL][1];
@@ -347,6 +365,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       }
       for (; k < k1; k += kWaves) {
         Vec<T, VEC> x = vload_pol<T, VEC>(base + int64_t(k) * ca.rs, ca.nt);
+        if (Op::kOrdered && k == 0)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) first[v] = x.v[v];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k - k0));
       }
@@ -354,7 +375,11 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       for (; k < k1; k += kWaves)
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
-          if (c0 + v < ca.C) acc[v] = Op::step(acc[v], base[int64_t(k) * ca.rs + v], int64_t(k - k0));
+          if (c0 + v < ca.C) {
+            const T x = base[int64_t(k) * ca.rs + v];
+            if (Op::kOrdered && k == 0) first[v] = x;
+            acc[v] = Op::step(acc[v], x, int64_t(k - k0));
+          }
     }
   }
   if (wv > 0) {
@@ -369,72 +394,10 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
       A r = acc[v];
 #pragma unroll
       for (int i = 0; i < kWaves - 1; ++i) r = Op::comb(r, part[i][lane * VEC + v]);
-      if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, base[v]);
+      if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, first[v]);  // wave 0 walked row 0
       const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
       write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
     }
-  }
-}
-
-// --------------------------------------------------------------------------------------------
-// wide col kernel: block = (outer, column group, tile) with all kRBlock lanes side by side over
-// kRBlock * VEC adjacent columns (4 KB of each row for f32), each lane walking the tile's rows
-// for its own VEC columns with UNROLL row loads in flight.  No cross-lane combine; every lane
-// writes its VEC results.
-template <class Op, class T, int VEC, int UNROLL, int WRITE>
-__global__ __launch_bounds__(kRBlock) void k_reduce_colw(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
-                                                         bool vec_ok) {
-  using A = typename Op::A;
-  const uint32_t b = blockIdx.x;
-  const uint32_t t = b % ca.tiles;
-  const uint32_t rest = b / ca.tiles;
-  const uint32_t cg = rest % ca.cgroups;
-  const uint32_t outer = rest / ca.cgroups;
-  const uint64_t c0 = (uint64_t(cg) * kRBlock + threadIdx.x) * VEC;
-  if (c0 >= ca.C) return;  // no barriers below
-  int64_t off[1];
-  row_offsets<1>(ca.ix, outer, off);
-  const T* base = a + off[0] + c0;
-  const uint64_t k0 = uint64_t(t) * ca.chunk;
-  const uint64_t k1 = k0 + ca.chunk < ca.R ? k0 + ca.chunk : ca.R;
-  const uint32_t n = k1 > k0 ? uint32_t(k1 - k0) : 0u;  // tile-relative indices below
-  const T* tb = base + int64_t(k0) * ca.rs;
-  A acc[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = Op::init();
-  if (vec_ok && c0 + VEC <= ca.C) {
-    uint32_t k = 0;
-    for (; k + UNROLL <= n; k += UNROLL) {
-      Vec<T, VEC> x[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) x[u] = vload_pol<T, VEC>(tb + int64_t(k + u) * ca.rs, ca.nt);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        T xs[UNROLL][1];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) xs[u][0] = x[u].v[v];
-        acc[v] = Op::template step_chunk<UNROLL, 1>(acc[v], xs, k, 1);
-      }
-    }
-    for (; k < n; ++k) {
-      Vec<T, VEC> x = vload_pol<T, VEC>(tb + int64_t(k) * ca.rs, ca.nt);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k));
-    }
-  } else {
-    for (uint32_t k = 0; k < n; ++k)
-#pragma unroll
-      for (int v = 0; v < VEC; ++v)
-        if (c0 + v < ca.C) acc[v] = Op::step(acc[v], tb[int64_t(k) * ca.rs + v], int64_t(k));
-  }
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    if (c0 + v >= ca.C) break;
-    A r = acc[v];
-    if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, base[v]);
-    const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
-    write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
   }
 }
 
