@@ -110,12 +110,12 @@ struct RowArgs {
 // One lane's share of a segment: lane l of a GROUP-lane group reduces elements l*VEC, l*VEC +
 // GROUP*VEC, ... of the n-element segment at tb (indices relative to tb).  Lane 0 also returns
 // the segment's first element in `first` (ordered reductions need it for the NaN-at-0 rule; it
-// is kept from the load instead of being read again at the end).
+// is kept from the load instead of being read again at the end).  The fold continues `acc`, and
+// ordered reductions record indices as base + (index in the segment).
 template <class Op, class T, int GROUP, int VEC, int UNROLL>
 __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, uint32_t n, int l, int64_t rs,
-                                                    bool nt, T& first) {
-  using A = typename Op::A;
-  A acc = Op::init();
+                                                    bool nt, T& first, typename Op::A acc = Op::init(),
+                                                    int64_t base = 0) {
   uint32_t k = uint32_t(l) * VEC;
   constexpr uint32_t stepk = uint32_t(GROUP) * VEC;
   const bool lead = l == 0;  // lane 0 starts at element 0
@@ -133,13 +133,13 @@ __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, ui
 #pragma unroll
         for (int v = 0; v < VEC; ++v) xs[u][v] = x[u].v[v];
       if (Op::kOrdered && lead && k == 0) first = xs[0][0];
-      acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk);
+      acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk, base);
     }
     for (; k + VEC <= n; k += stepk) {  // whole vectors left
       Vec<T, VEC> x = vload_pol<T, VEC>(tb + k, nt);
       if (Op::kOrdered && lead && k == 0) first = x.v[0];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x.v[v], int64_t(k + v));
+      for (int v = 0; v < VEC; ++v) acc = Op::step(acc, x.v[v], base + int64_t(k + v));
     }
     if (k < n) {  // the last, partial vector of the tile
 #pragma unroll
@@ -147,7 +147,7 @@ __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, ui
         if (k + v < n) {
           const T x = tb[k + v];
           if (Op::kOrdered && lead && k + v == 0) first = x;
-          acc = Op::step(acc, x, int64_t(k + v));
+          acc = Op::step(acc, x, base + int64_t(k + v));
         }
     }
   } else {
@@ -157,12 +157,12 @@ __device__ inline typename Op::A accumulate_segment(const T* __restrict__ tb, ui
       for (int u = 0; u < UNROLL; ++u) x[u] = tb[int64_t(k + u * stepk) * rs];
       if (Op::kOrdered && lead && k == 0) first = x[0];
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], int64_t(k + u * stepk));
+      for (int u = 0; u < UNROLL; ++u) acc = Op::step(acc, x[u], base + int64_t(k + u * stepk));
     }
     for (; k < n; k += stepk) {
       const T x = tb[int64_t(k) * rs];
       if (Op::kOrdered && lead && k == 0) first = x;
-      acc = Op::step(acc, x, int64_t(k));
+      acc = Op::step(acc, x, base + int64_t(k));
     }
   }
   return acc;
@@ -201,19 +201,48 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
 // (output, tile) blocks; each publishes its tile's accumulator (publish.hpp) and exits.  Blocks
 // out_size*tiles + o, the last of the grid, are combiners: the dispatcher hands them out after
 // every streaming block, so they poll the slots while the last tiles are still streaming and
-// finish right after the last publish.  Lane l of a combiner owns tiles l, l + 512, ... (at most
-// kFusedPerLane), waits until all of them are published (a bounded poll), folds them in ascending
-// order, and the block tree combines the lanes: a fixed order, independent of timing.  A combiner
-// holds one block slot; with at most kFusedMaxOutputs of them the streaming blocks always find
-// room, so the waits end.  Every slot read is cleared again, leaving the workspace zero.
-// Workspace: out_size * tiles * W slot words.
-constexpr int kFusedPerLane = 8;
+// finish right after the last publish.  Lane l of a combiner owns tiles l, l + 512, ... (PER of
+// them at most, a template parameter so the slot registers do not inflate the streaming blocks'
+// register budget), waits until all of them are published (a bounded poll), folds them in
+// ascending order, and the block tree combines the lanes: a fixed order, independent of timing.
+// A combiner holds one block slot; with at most kFusedMaxOutputs of them the streaming blocks
+// always find room, so the waits end.  Every slot read is cleared again, leaving the workspace
+// zero.  Workspace: out_size * tiles * W slot words.
 constexpr size_t kFusedMaxOutputs = 64;
-constexpr size_t kFusedMaxTiles = 2048;  // <= kFusedPerLane * kRowBS
+constexpr size_t kFusedMaxTiles = 2048;  // <= 8 * kRowBS (the largest PER dispatched)
 struct FusedArgs {
   uint64_t* slots;
   uint32_t spin_limit;
 };
+
+// Gathers the published W-word slots lane, lane + kRowBS, ... (below `count`) into v: all
+// outstanding slots' words are loaded together, the ready ones kept, the rest polled again.
+template <int W, int PER>
+__device__ inline void gather_published(const uint64_t* slots, uint32_t count, uint32_t spin_limit,
+                                        uint64_t (&v)[PER][W]) {
+  uint32_t pending = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (threadIdx.x + j * kRowBS < count) pending |= 1u << j;
+#pragma unroll
+    for (int i = 0; i < W; ++i) v[j][i] = 0;
+  }
+  for (uint32_t spins = 0; pending != 0 && spins < spin_limit; ++spins) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (pending & (1u << j))
+#pragma unroll
+        for (int i = 0; i < W; ++i) v[j][i] = ld_relaxed(slots + uint64_t(threadIdx.x + j * kRowBS) * W + i);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      bool ready = true;
+#pragma unroll
+      for (int i = 0; i < W; ++i) ready = ready && (v[j][i] & kTag);
+      if (ready) pending &= ~(1u << j);
+    }
+    if (pending) __builtin_amdgcn_s_sleep(2);
+  }
+}
 
 // a tile's accumulator (tile-relative int32 index) as the final's accumulator (absolute index)
 template <class Op, class OpF>
@@ -225,7 +254,7 @@ __device__ inline typename OpF::A to_final(const typename Op::A& x, int64_t k0) 
   }
 }
 
-template <class Op, class OpF, class T, int VEC, int UNROLL>
+template <class Op, class OpF, class T, int VEC, int UNROLL, int PER>
 __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict__ a, RowArgs ra, RedOut<T> out,
                                                              FusedArgs fa) {
   using A = typename Op::A;
@@ -256,36 +285,12 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
   // combiner of output o
   const uint64_t o = w - ra.nwork;
   uint64_t* row_slots = fa.slots + o * ra.tiles * W;
-  uint64_t v[kFusedPerLane][W] = {};
-  uint32_t pending = 0;
-#pragma unroll
-  for (int j = 0; j < kFusedPerLane; ++j)
-    if (threadIdx.x + j * kRowBS < ra.tiles) pending |= 1u << j;
-  for (uint32_t spins = 0; pending != 0 && spins < fa.spin_limit; ++spins) {
-    uint64_t u[kFusedPerLane][W];
-#pragma unroll
-    for (int j = 0; j < kFusedPerLane; ++j)  // every outstanding slot's words in flight together
-      if (pending & (1u << j))
-#pragma unroll
-        for (int i = 0; i < W; ++i) u[j][i] = ld_relaxed(row_slots + uint64_t(threadIdx.x + j * kRowBS) * W + i);
-#pragma unroll
-    for (int j = 0; j < kFusedPerLane; ++j) {
-      if (!(pending & (1u << j))) continue;
-      bool ready = true;
-#pragma unroll
-      for (int i = 0; i < W; ++i) ready = ready && (u[j][i] & kTag);
-      if (ready) {
-#pragma unroll
-        for (int i = 0; i < W; ++i) v[j][i] = u[j][i];
-        pending &= ~(1u << j);
-      }
-    }
-    if (pending) __builtin_amdgcn_s_sleep(2);
-  }
+  uint64_t v[PER][W];
+  gather_published<W, PER>(row_slots, ra.tiles, fa.spin_limit, v);
   AF r = OpF::init();
   A first{};
 #pragma unroll
-  for (int j = 0; j < kFusedPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const uint32_t tt = threadIdx.x + j * kRowBS;
     if (tt >= ra.tiles) break;
     uint32_t s[W];
@@ -305,6 +310,111 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
       if (first.idx >= 0 && is_nan(first.val)) r = to_final<Op, OpF>(first, 0);
     }
     write_result<OpF, T, kWriteFinal>(out, o, r, 0);
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// Whole-array reduction (one output) on a persistent grid: block b of G streams chunks b, b+G,
+// b+2G, ... (chunk = one round of the block, 512 lanes x UNROLL x 16 bytes), folding each chunk
+// into its lanes' running accumulators in that fixed order; then blocks publish and a combiner
+// block (index G) folds the G block results as in k_reduce_row_fused.  Ordered ops fold a chunk
+// with tile-relative int32 indices and move it into an int64 running accumulator per lane.
+template <class Op, class OpF, class T, int VEC, int UNROLL, int PER>
+__global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict__ a, uint64_t n, uint32_t grid,
+                                                             RedOut<T> out, FusedArgs fa) {
+  using A = typename Op::A;
+  using AF = typename OpF::A;
+  static_assert(sizeof(AF) % 4 == 0, "accumulator must split into 32-bit slices");
+  constexpr int W = int(sizeof(AF) / 4);
+  constexpr uint64_t kChunk = uint64_t(kRowBS) * UNROLL * VEC;
+  const uint32_t b = blockIdx.x;
+  if (b < grid) {
+    AF acc = OpF::init();
+    T first{};
+    const uint64_t nchunks = (n + kChunk - 1) / kChunk;
+    // The lane's running accumulator (absolute int64 indices) continues from chunk to chunk, so
+    // an ordered fold searches a chunk only when the chunk beats it.  Whole chunks are software
+    // pipelined: the next chunk's loads are in flight while the current one is folded.
+    constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
+    const uint64_t whole = n / kChunk;
+    uint64_t c = b;
+    Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers: no register copies between chunks
+    auto load = [&](uint64_t cc, Vec<T, VEC>(&dst)[UNROLL]) {
+      const T* p = a + cc * kChunk + threadIdx.x * VEC;
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) dst[u] = vload_nt<T, VEC>(p + u * stepk);
+    };
+    auto fold = [&](uint64_t cc, const Vec<T, VEC>(&src)[UNROLL]) {
+      T xs[UNROLL][VEC];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) xs[u][v] = src[u].v[v];
+      if (cc == 0) first = xs[0][0];  // lane 0 holds element 0
+      acc = OpF::template step_chunk<UNROLL, VEC>(acc, xs, threadIdx.x * VEC, stepk, int64_t(cc * kChunk));
+    };
+    // the steady-state loop prefetches unconditionally (a conditional prefetch would make the
+    // wait before each fold cover the prefetch too); the last one or two chunks are peeled
+    const uint64_t mine = c < whole ? (whole - c + grid - 1) / grid : 0;  // whole chunks of this block
+    if (mine > 0) {
+      load(c, x);
+      uint64_t i = 0;
+      for (; i + 2 < mine; i += 2) {
+        load(c + grid, y);
+        fold(c, x);
+        load(c + 2 * grid, x);
+        fold(c + grid, y);
+        c += 2 * grid;
+      }
+      if (i + 1 < mine) {
+        load(c + grid, y);
+        fold(c, x);
+        fold(c + grid, y);
+      } else {
+        fold(c, x);
+      }
+      c = b + mine * grid;  // the first chunk index past this block's whole chunks
+    }
+    if (c == whole && whole * kChunk < n) {  // the last, partial chunk
+      T f{};
+      acc = accumulate_segment<OpF, T, kRowBS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
+                                                            true, f, acc, int64_t(c * kChunk));
+      if (c == 0) first = f;
+    }
+    acc = group_reduce<OpF, kRowBS>(acc);
+    if (threadIdx.x == 0) {
+      if (b == 0 && n > 0) acc = absorb_first<OpF, T>(acc, first);
+      uint32_t s[W];
+      __builtin_memcpy(s, &acc, sizeof(AF));
+      publish_slices<W>(fa.slots + uint64_t(b) * W, s);
+    }
+    return;
+  }
+  // combiner: lane l folds block results l, l + 512, ... (PER of them at most)
+  uint64_t v[PER][W];
+  gather_published<W, PER>(fa.slots, grid, fa.spin_limit, v);
+  AF r = OpF::init();
+  AF first{};
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t bb = threadIdx.x + j * kRowBS;
+    if (bb >= grid) break;
+    uint32_t s[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) s[i] = uint32_t(v[j][i]);
+    AF x;
+    __builtin_memcpy(&x, s, sizeof(AF));
+    if (bb == 0) first = x;
+    r = OpF::comb(r, x);
+#pragma unroll
+    for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
+  }
+  r = group_reduce<OpF, kRowBS>(r);
+  if (threadIdx.x == 0) {
+    if constexpr (Op::kOrdered) {
+      if (first.idx == 0 && is_nan(first.val)) r = first;  // block 0 absorbed a NaN at position 0
+    }
+    write_result<OpF, T, kWriteFinal>(out, 0, r, 0);
   }
 }
 
@@ -597,19 +707,26 @@ template <class T> inline RedOut<T> vout(T* c) { return RedOut<T>{c, nullptr, 0.
 template <class T> inline RedOut<T> iout(int64_t* c) { return RedOut<T>{nullptr, c, 0.0, kFinPlain}; }
 template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c, nullptr, cnt, kFinMean}; }
 
+template <class Op, class OpF, class T>
+bool launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
+                             hipStream_t st);
+
 // the fused single launch for a row-kind reduction split into `tiles` tiles; false (nothing
 // launched) when the shape does not take the 512-lane block path or the workspace is too small
 template <class Op, class OpF, class T>
 bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                          size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
   if (out_size == 0 || out_size > kFusedMaxOutputs || axis_len == 0 || tiles < 2 || ws == nullptr) return false;
-  // a combiner lane folds at most kFusedPerLane tiles; 2048 tiles measured best for 64M f32
+  // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
   if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
   if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return false;
   for (int d = 0; d < p.ond; ++d)
     if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return false;
+  // one output over one contiguous run: the persistent grid (1024 blocks measured best for 64M
+  // f32: sum 6.5, argmax 6.1 TB/s against 6.1 / 5.9 with one block per tile)
+  if (out_size == 1 && launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, 1024, ws, ws_bytes, st)) return true;
   constexpr int V = rvec<T>();
   uint64_t chunk = ceil_div(ceil_div(p.R, tiles), uint64_t(V)) * V;
   if (chunk * sizeof(T) < 16384 || chunk >= (uint64_t(1) << 31)) return false;
@@ -628,7 +745,35 @@ bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shap
   fa.slots = static_cast<uint64_t*>(ws);
   fa.spin_limit = 1u << 24;
   // streaming blocks first, then one combiner per output
-  k_reduce_row_fused<Op, OpF, T, V, 4><<<dim3(unsigned(ra.nwork + out_size)), kRowBS, 0, st>>>(a, ra, out, fa);
+  const dim3 grid(unsigned(ra.nwork + out_size));
+  switch (ceil_div(tiles, uint64_t(kRowBS))) {
+    case 1: k_reduce_row_fused<Op, OpF, T, V, 4, 1><<<grid, kRowBS, 0, st>>>(a, ra, out, fa); break;
+    case 2: k_reduce_row_fused<Op, OpF, T, V, 4, 2><<<grid, kRowBS, 0, st>>>(a, ra, out, fa); break;
+    default: k_reduce_row_fused<Op, OpF, T, V, 4, 4><<<grid, kRowBS, 0, st>>>(a, ra, out, fa); break;
+  }
+  return true;
+}
+
+// whole-array reduction of `n` contiguous, 16-byte aligned elements on a persistent grid of
+// `grid` blocks plus a combiner; false when not applicable (nothing launched)
+template <class Op, class OpF, class T>
+bool launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
+                             hipStream_t st) {
+  constexpr int V = rvec<T>();
+  constexpr uint64_t kChunk = uint64_t(kRowBS) * 4 * V;
+  if (n == 0 || ws == nullptr || !al16(a)) return false;
+  const uint64_t nchunks = ceil_div(n, kChunk);
+  if (grid > nchunks) grid = uint32_t(nchunks);
+  if (grid < 2 || grid > 2 * kRowBS) return false;
+  const uint64_t W = sizeof(typename OpF::A) / 4;
+  if (uint64_t(grid) * W * 8 > ws_bytes) return false;
+  FusedArgs fa{};
+  fa.slots = static_cast<uint64_t*>(ws);
+  fa.spin_limit = 1u << 24;
+  if (grid <= kRowBS)
+    k_reduce_all_fused<Op, OpF, T, V, 4, 1><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
+  else
+    k_reduce_all_fused<Op, OpF, T, V, 4, 2><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
   return true;
 }
 

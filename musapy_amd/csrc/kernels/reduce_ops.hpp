@@ -59,15 +59,15 @@ template <> struct SumAcc<int64_t> { using A = uint64_t; };  // two's-complement
 template <> struct SumAcc<c64> { using A = c128; };
 template <> struct SumAcc<c128> { using A = c128; };
 
-// A chunk of U x V elements one lane loaded together: element (u, v) sits at tile-relative index
-// k + u * stepk + v, so (u, v) in lexicographic order is increasing index.  The default folds the
-// chunk element by element in that order.
+// A chunk of U x V elements one lane loaded together: element (u, v) sits at index
+// base + k + u * stepk + v, so (u, v) in lexicographic order is increasing index.  The default
+// folds the chunk element by element in that order.
 template <class Op, class A, class T, int U, int V>
-__device__ inline A fold_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+__device__ inline A fold_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk, int64_t base) {
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
-    for (int v = 0; v < V; ++v) acc = Op::step(acc, x[u][v], int64_t(k + u * stepk + v));
+    for (int v = 0; v < V; ++v) acc = Op::step(acc, x[u][v], base + int64_t(k + u * stepk + v));
   return acc;
 }
 
@@ -80,8 +80,8 @@ struct OpSum {
   __device__ static A step(A acc, T v, int64_t) { return acc + A(v); }
   __device__ static A comb(A a, A b) { return a + b; }
   template <int U, int V>
-  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
-    return fold_chunk<OpSum, A, T, U, V>(acc, x, k, stepk);
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk, int64_t base = 0) {
+    return fold_chunk<OpSum, A, T, U, V>(acc, x, k, stepk, base);
   }
 };
 template <> __device__ inline c128 OpSum<c64>::init() { return c128{0.0, 0.0}; }
@@ -104,8 +104,8 @@ struct OpProd {
   __device__ static A step(A acc, T v, int64_t) { return acc * A(v); }
   __device__ static A comb(A a, A b) { return a * b; }
   template <int U, int V>
-  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
-    return fold_chunk<OpProd, A, T, U, V>(acc, x, k, stepk);
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk, int64_t base = 0) {
+    return fold_chunk<OpProd, A, T, U, V>(acc, x, k, stepk, base);
   }
 };
 __device__ inline c128 cmul(c128 a, c128 b) {
@@ -155,7 +155,7 @@ struct OpExt {
   // NaN), and equality also matches +0 against -0, so the kept bits are the first zero's.  A tie
   // with the running result keeps the running (lower) index.
   template <int U, int V>
-  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk) {
+  __device__ static A step_chunk(A acc, const T (&x)[U][V], uint32_t k, uint32_t stepk, int64_t base = 0) {
     T m = x[0][0];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -173,7 +173,7 @@ struct OpExt {
             off = u * stepk + v;
             val = x[u][v];
           }
-      acc = A{val, I(k + off)};
+      acc = A{val, I(base + int64_t(k + off))};
     }
     return acc;
   }
