@@ -157,6 +157,20 @@ def all_config_ops(ms):
          + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
     Z = _copies(ms, z, K)
     ops.append(("C5 c64 sum axis=(1,2)", lambda i: ms.sum(Z[i % K], axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128))
+    # widened rows: comparisons (1-byte bool output) and complex elementwise
+    M = 16 * 1024 * 1024
+    ops.append(("cmp lt f32 64M -> bool", lambda i: ms.lt(A64[i % K], B64[i % K]), 9 * 67_108_864))
+    ops.append(("cmp eq f64 16M -> bool", lambda i: ms.eq(s[i % K], c[i % K]), 17 * N))
+    Z2 = [ms.neg(Z[(k + 1) % K]) for k in range(K)]
+    ops.append(("cmp eq c64 16M -> bool", lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M))
+    ops.append(("c64 mul 16M", lambda i: ms.mul(Z[i % K], Z2[i % K]), 24 * M))
+    ops.append(("c64 div 16M", lambda i: ms.div(Z[i % K], Z2[i % K]), 24 * M))
+    ops.append(("c64 abs 16M -> f32", lambda i: ms.abs(Z[i % K]), 12 * M))
+    ops.append(("astype f32->c64 64M", lambda i: ms.astype(A64[i % K], "c64"), 12 * 67_108_864))
+    W = [ms.astype(Z[k], "c128") for k in range(K)]
+    W2 = [ms.astype(Z2[k], "c128") for k in range(K)]
+    ops.append(("c128 mul 16M", lambda i: ms.mul(W[i % K], W2[i % K]), 48 * M))
+    ops.append(("c128 div 16M", lambda i: ms.div(W[i % K], W2[i % K]), 48 * M))
     return ops
 
 

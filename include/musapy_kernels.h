@@ -108,6 +108,46 @@ typedef struct { double re; double im; } musapy_c128_t;
 void musapy_cast_f32_bf16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
 void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
 
+/* ---- comparison elementwise: 0/1 bytes over broadcast strides (IEEE: NaN compares unequal) ---- */
+/* kernels.rs:84 */ void musapy_eq_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:85 */ void musapy_eq_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:86 */ void musapy_ne_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:87 */ void musapy_ne_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:88 */ void musapy_lt_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:89 */ void musapy_lt_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:90 */ void musapy_gt_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:91 */ void musapy_gt_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:92 */ void musapy_le_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:93 */ void musapy_le_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:94 */ void musapy_ge_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:95 */ void musapy_ge_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* complex: equal when both the real and the imaginary parts are equal */
+/* kernels.rs:114 */ void musapy_eq_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:115 */ void musapy_eq_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:116 */ void musapy_ne_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:117 */ void musapy_ne_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, uint8_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+
+/* ---- complex elementwise over interleaved re/im elements ----
+ * Component formulas evaluated in f64 without fma contraction; c64 results narrowed once. */
+/* kernels.rs:102 */ void musapy_add_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:103 */ void musapy_add_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:104 */ void musapy_sub_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:105 */ void musapy_sub_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:106 */ void musapy_mul_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:107 */ void musapy_mul_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:108 */ void musapy_div_c64_v2(const musapy_c64_t* a, const musapy_c64_t* b, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:109 */ void musapy_div_c128_v2(const musapy_c128_t* a, const musapy_c128_t* b, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
+/* kernels.rs:110 */ void musapy_neg_c64_v2(const musapy_c64_t* a, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:111 */ void musapy_neg_c128_v2(const musapy_c128_t* a, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:112 */ void musapy_abs_c64_v2(const musapy_c64_t* a, float* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:113 */ void musapy_abs_c128_v2(const musapy_c128_t* a, double* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* real -> complex (re = src, im = +0) and c64 -> c128 */
+/* kernels.rs:119 */ void musapy_cast_f32_c64_v2(const float* a, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:120 */ void musapy_cast_f32_c128_v2(const float* a, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:121 */ void musapy_cast_f64_c64_v2(const double* a, musapy_c64_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:122 */ void musapy_cast_f64_c128_v2(const double* a, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+/* kernels.rs:124 */ void musapy_cast_c64_c128_v2(const musapy_c64_t* a, musapy_c128_t* c, int ndim, const size_t* shape, const ssize_t* a_strides, hipStream_t stream);
+
 /* ---- reduction (single pass) ---- */
 /* kernels.rs:139 */ void musapy_sum_i64_v2(const int64_t* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
 /* kernels.rs:140 */ void musapy_sum_f32_v2(const float* a, float* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);

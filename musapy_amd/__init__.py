@@ -8,6 +8,7 @@ kernel library ``libmusapy_hip.so``; importing fails loudly when it has not been
 """
 from __future__ import annotations
 
+import builtins as _builtins
 import os as _os
 
 import numpy as _np
@@ -24,6 +25,7 @@ from ._core import (  # noqa: F401
     Array, MusapyError, DeviceError, DeviceNotConfiguredError, DtypeError, ShapeError, MemoryError,
     OutOfMemoryError, StreamError, KernelError,
     add, sub, mul, div, pow, sin, cos, exp, log, abs, sign, neg, clamp, astype,
+    eq, ne, lt, gt, le, ge,
     sum, prod, max, min, mean, argmax, argmin, cumsum,
     transpose, flip, index_select, contiguous,
     set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats, empty_cache,
@@ -31,25 +33,28 @@ from ._core import (  # noqa: F401
 )
 
 __all__ = [
-    "Array", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp", "log",
-    "abs", "sign", "neg", "clamp", "astype", "sum", "prod", "max", "min", "mean", "argmax", "argmin",
-    "cumsum", "transpose", "permute", "flip", "slice", "index_select", "contiguous", "Stream", "stream",
-    "current_stream", "synchronize",
+    "Array", "Dtype", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp",
+    "log", "abs", "sign", "neg", "clamp", "astype", "eq", "ne", "lt", "gt", "le", "ge", "sum", "prod", "max",
+    "min", "mean", "argmax", "argmin", "cumsum", "transpose", "permute", "flip", "slice", "index_select",
+    "contiguous", "Stream", "stream", "current_stream", "synchronize",
 ]
 
-# dtype names (musapy exposes ms.float32 etc. as dtype objects; here they are the dtype strings)
-bool_ = "bool"
-int8, int16, int32, int64 = "i8", "i16", "i32", "i64"
-uint8, uint16, uint32, uint64 = "u8", "u16", "u32", "u64"
-float16, float32, float64, bfloat16 = "f16", "f32", "f64", "bf16"
-complex64, complex128 = "c64", "c128"
+# dtype constants: Dtype objects that compare equal to their names and aliases
+# (rust/musapy-python/src/dtype.rs:149-190; python/musapy/__init__.py exports `bool` as `bool_`)
+Dtype = _core.Dtype
+bool_ = getattr(_core, "bool")
+int8, int16, int32, int64 = _core.int8, _core.int16, _core.int32, _core.int64
+uint8, uint16, uint32, uint64 = _core.uint8, _core.uint16, _core.uint32, _core.uint64
+float16, float32, float64, bfloat16 = _core.float16, _core.float32, _core.float64, _core.bfloat16
+complex64, complex128 = _core.complex64, _core.complex128
 
 _NP_OF = {"bool": _np.bool_, "i8": _np.int8, "i16": _np.int16, "i32": _np.int32, "i64": _np.int64,
           "u8": _np.uint8, "u16": _np.uint16, "u32": _np.uint32, "u64": _np.uint64, "f16": _np.float16,
           "f32": _np.float32, "f64": _np.float64, "c64": _np.complex64, "c128": _np.complex128}
 _ALIASES = {"float32": "f32", "float64": "f64", "float16": "f16", "bfloat16": "bf16", "int8": "i8",
             "int16": "i16", "int32": "i32", "int64": "i64", "uint8": "u8", "uint16": "u16",
-            "uint32": "u32", "uint64": "u64", "complex64": "c64", "complex128": "c128", "bool_": "bool"}
+            "uint32": "u32", "uint64": "u64", "complex64": "c64", "complex128": "c128", "bool_": "bool",
+            "b1": "bool", "bool8": "bool", "half": "f16", "single": "f32", "double": "f64"}
 
 
 def _norm_dtype(d) -> str:
@@ -57,8 +62,18 @@ def _norm_dtype(d) -> str:
         return None
     if isinstance(d, _np.dtype) or (isinstance(d, type) and issubclass(d, _np.generic)):
         d = _np.dtype(d).name
-    d = str(d)
-    return _ALIASES.get(d, d)
+    if not isinstance(d, (str, Dtype)):
+        raise TypeError("dtype must be a Dtype instance or a dtype string (e.g. 'f32', 'float32')")
+    d = str(d).lower()
+    d = _ALIASES.get(d, d)
+    if d not in _NP_OF and d != "bf16":
+        raise ValueError(f"unknown dtype: {d}")
+    return d
+
+
+def _c_order(x):
+    """C-contiguous copy when needed; unlike numpy.ascontiguousarray it keeps 0-d arrays 0-d."""
+    return x if x.flags.c_contiguous else x.copy(order="C")
 
 
 def _contains_complex(x) -> bool:
@@ -87,13 +102,12 @@ def array(data, dtype=None, device=None) -> Array:
             raise DtypeError("bf16 arrays are created from raw uint16 bit patterns")
     else:
         host = _np.asarray(data, dtype=_NP_OF[dt])
-    return _core._from_numpy(_np.ascontiguousarray(host), dt, device)
+    return _core._from_numpy(_c_order(host), dt, device)
 
 
 def from_numpy(x, device=None) -> Array:
     """Copy a numpy array (any dtype musapy knows) to the device, keeping its dtype."""
-    x = _np.ascontiguousarray(x)
-    name = {v: k for k, v in _ALIASES.items()}
+    x = _c_order(_np.asarray(x))
     dt = _ALIASES.get(x.dtype.name, x.dtype.name)
     return _core._from_numpy(x, dt, device)
 
@@ -135,6 +149,39 @@ def _repr(self: Array) -> str:
     return f"Array(shape={self.shape}, dtype={self.dtype}, device={self.device})"
 
 
+def _getitem(self: Array, key) -> Array:
+    """Basic indexing as zero-copy views (rust/musapy-python/src/array.rs:225-450, view path):
+    an int selects along an axis and drops it, a slice keeps it; a tuple applies item by item.
+    Array indices (boolean masks, fancy indexing) are outside this backend's path."""
+    items = key if isinstance(key, tuple) else (key,)
+    if self.ndim == 0:
+        raise IndexError("too many indices for 0-dim array")
+    if len(items) > self.ndim:
+        raise IndexError("too many indices for array")
+    cur, dim = self, 0
+    for it in items:
+        size = cur.shape[dim]
+        if isinstance(it, _builtins.slice):
+            start, stop, step = it.indices(size)
+            if step <= 0:
+                raise ValueError("slice step must be positive")
+            ranges = [(0, d, 1) for d in cur.shape]
+            ranges[dim] = (start, _builtins.max(start, stop), step)
+            cur = slice(cur, ranges)
+            dim += 1
+        elif isinstance(it, (int, _np.integer)) and not isinstance(it, bool):
+            i = int(it)
+            if i < 0:
+                i += size
+            if i < 0 or i >= size:
+                raise IndexError(f"index {int(it)} out of bounds for dimension (size {size})")
+            cur = index_select(cur, dim, i)
+        else:
+            raise TypeError("index must be an integer or slice (array indices are not supported by this backend)")
+    return cur
+
+
+Array.__getitem__ = _getitem
 Array.tolist = _tolist
 Array.item = _item
 Array.__repr__ = _repr

@@ -66,8 +66,9 @@ __global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict_
   }
 }
 
-template <int VEC, int UNROLL, class F, class T>
-__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __restrict__ c, uint64_t n, F f) {
+// TO: the output element type (T for arithmetic, uint8_t for comparisons)
+template <int VEC, int UNROLL, class F, class T, class TO = T>
+__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __restrict__ c, uint64_t n, F f) {
   constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
   const uint64_t base = uint64_t(blockIdx.x) * kTile;
   const int t = threadIdx.x;
@@ -95,10 +96,10 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, T* __r
     }
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      Vec<T, VEC> vc;
+      Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k], vb[u].v[k]);
-      vstore_out<T, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+      vstore_out<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
     }
   } else {
     for (uint64_t i = base + t; i < n; i += kBlock)
@@ -158,8 +159,8 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
   }
 }
 
-template <int VEC, int UNROLL, class F, class T>
-__global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<T> b, int64_t sb, T* __restrict__ c,
+template <int VEC, int UNROLL, class F, class T, class TO = T>
+__global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<T> b, int64_t sb, TO* __restrict__ c,
                                                         RowIndexer<3> ix, FastDiv gpr, uint32_t L, uint32_t items,
                                                         bool aligned, F f) {
   const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
@@ -175,12 +176,12 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
     T x[VEC], y[VEC];
     load_item<VEC, T>(a.p + off[1], a.mode, sa, col, L, full && aligned, a.nt, x);
     load_item<VEC, T>(b.p + off[2], b.mode, sb, col, L, full && aligned, b.nt, y);
-    T* cp = c + off[0] + col;
+    TO* cp = c + off[0] + col;
     if (full && aligned) {
-      Vec<T, VEC> v;
+      Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k], y[k]);
-      vstore_out<T, VEC>(cp, v);
+      vstore_out<TO, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -222,8 +223,8 @@ struct TileArgs {
   bool a_inv, b_inv;  // operand does not depend on the row
 };
 
-template <int VEC, class F, class T>
-__global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In<T> b, int64_t sb, T* __restrict__ c,
+template <int VEC, class F, class T, class TO = T>
+__global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In<T> b, int64_t sb, TO* __restrict__ c,
                                                          TileArgs ta, F f) {
   const uint32_t col = (blockIdx.x * kBlock + threadIdx.x) * VEC;
   if (col >= ta.L) return;
@@ -260,12 +261,12 @@ __global__ __launch_bounds__(kBlock) void k_binary_tiles(In<T> a, int64_t sa, In
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       if (r + u >= r1) break;
-      T* cp = c + oc[u] + col;
+      TO* cp = c + oc[u] + col;
       if (vec) {
-        Vec<T, VEC> v;
+        Vec<TO, VEC> v;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) v.v[k] = f(xa[u][k], xb[u][k]);
-        vstore_out<T, VEC>(cp, v);
+        vstore_out<TO, VEC>(cp, v);
       } else {
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
@@ -383,9 +384,9 @@ __global__ __launch_bounds__(kBlock) void k_unary_generic(const TA* __restrict__
   }
 }
 
-template <class F, class T>
+template <class F, class T, class TO = T>
 __global__ __launch_bounds__(kBlock) void k_binary_generic(const T* __restrict__ a, const T* __restrict__ b,
-                                                           T* __restrict__ c, NdMeta64 m, uint64_t n, F f) {
+                                                           TO* __restrict__ c, NdMeta64 m, uint64_t n, F f) {
   for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += uint64_t(gridDim.x) * kBlock) {
     int64_t off[3];
     nd_offsets(m, i, 3, off);
@@ -551,8 +552,8 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
   k_unary_generic<F, TO, TA><<<grid_generic(p.numel), kBlock, 0, st>>>(a, c, make_meta64(p), p.numel, f);
 }
 
-template <class F, class T>
-void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, const ssize_t* as, const ssize_t* bs,
+template <class F, class T, class TO = T>
+void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape, const ssize_t* as, const ssize_t* bs,
                    hipStream_t st, F f) {
   Plan p;
   const ssize_t* ins[2] = {as, bs};
@@ -562,13 +563,15 @@ void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, 
   const bool nt = (operand_elems(p, 1) + operand_elems(p, 2)) * sizeof(T) >= kStreamLoadBytes;
   if (nd == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1) && (p.stride[2][0] == 0 || p.stride[2][0] == 1)) {
     In<T> ia{a, mode_of(p.stride[1][0]), nt}, ib{b, mode_of(p.stride[2][0]), nt};
-    bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a)) && (ib.mode == kModeScalar || aligned16(b));
+    constexpr uintptr_t kOutAlign = sizeof(TO) * V < 16 ? sizeof(TO) * V : 16;  // one output vector
+    bool vec_ok = (reinterpret_cast<uintptr_t>(c) % kOutAlign) == 0 && (ia.mode == kModeScalar || aligned16(a)) &&
+                  (ib.mode == kModeScalar || aligned16(b));
     if (vec_ok) {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
-      k_binary_flat<V, kFlatUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+      k_binary_flat<V, kFlatUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
     } else {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
-      k_binary_flat<1, kUnroll, F, T><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+      k_binary_flat<1, kUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
     }
     return;
   }
@@ -576,7 +579,7 @@ void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, 
     const uint32_t L = uint32_t(p.shape[nd - 1]);
     const int64_t sa = p.stride[1][nd - 1], sb = p.stride[2][nd - 1];
     In<T> ia{a, mode_of(sa), nt}, ib{b, mode_of(sb), nt};
-    bool al = rows_aligned<T, T, T>(p, V, c, a, b);
+    bool al = rows_aligned<TO, T, T>(p, V, c, a, b);
     uint32_t gpr = (L + V - 1) / V;
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<3> ix = make_row_indexer<3>(p);
@@ -598,14 +601,15 @@ void launch_binary(const T* a, const T* b, T* c, int ndim, const size_t* shape, 
       if ((ta.rows + rb - 1) / rb > 65535) rb = (ta.rows + 65534) / 65535;
       ta.rb = uint32_t(rb);
       const uint32_t gy = uint32_t((ta.rows + rb - 1) / rb);
-      k_binary_tiles<V, F, T><<<dim3(gx, gy), kBlock, 0, st>>>(ia, sa, ib, sb, c, ta, f);
+      k_binary_tiles<V, F, T, TO><<<dim3(gx, gy), kBlock, 0, st>>>(ia, sa, ib, sb, c, ta, f);
       return;
     }
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-    k_binary_rows<V, kUnroll, F, T><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al, f);
+    k_binary_rows<V, kUnroll, F, T, TO><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al,
+                                                                 f);
     return;
   }
-  k_binary_generic<F, T><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
+  k_binary_generic<F, T, TO><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
 }
 
 template <class F, class TC, class TA, class TB>
@@ -674,6 +678,63 @@ MPY_BINARY(div, DivF)
 MPY_BINARY(pow, PowF)
 #undef MPY_BINARY
 
+// comparisons (kernels.rs:84-95, 114-117): the binary kernels with a 0/1-byte output
+#define MPY_COMPARE(NAME, F)                                                                                \
+  void musapy_##NAME##_f32_v2(const float* a, const float* b, uint8_t* c, int ndim, const size_t* shape,    \
+                              const ssize_t* as, const ssize_t* bs, hipStream_t st) {                      \
+    launch_binary<F, float, uint8_t>(a, b, c, ndim, shape, as, bs, st, F{});                               \
+  }                                                                                                         \
+  void musapy_##NAME##_f64_v2(const double* a, const double* b, uint8_t* c, int ndim, const size_t* shape,  \
+                              const ssize_t* as, const ssize_t* bs, hipStream_t st) {                      \
+    launch_binary<F, double, uint8_t>(a, b, c, ndim, shape, as, bs, st, F{});                              \
+  }
+MPY_COMPARE(eq, EqF)
+MPY_COMPARE(ne, NeF)
+MPY_COMPARE(lt, LtF)
+MPY_COMPARE(gt, GtF)
+MPY_COMPARE(le, LeF)
+MPY_COMPARE(ge, GeF)
+#undef MPY_COMPARE
+#define MPY_COMPARE_C(NAME, F, SN, C)                                                                       \
+  void musapy_##NAME##_##SN##_v2(const C* a, const C* b, uint8_t* c, int ndim, const size_t* shape,         \
+                                 const ssize_t* as, const ssize_t* bs, hipStream_t st) {                   \
+    launch_binary<F, C, uint8_t>(a, b, c, ndim, shape, as, bs, st, F{});                                   \
+  }
+MPY_COMPARE_C(eq, CEqF, c64, c64)
+MPY_COMPARE_C(eq, CEqF, c128, c128)
+MPY_COMPARE_C(ne, CNeF, c64, c64)
+MPY_COMPARE_C(ne, CNeF, c128, c128)
+#undef MPY_COMPARE_C
+
+// complex arithmetic (kernels.rs:102-113)
+#define MPY_BINARY_C(NAME, F)                                                                               \
+  void musapy_##NAME##_c64_v2(const c64* a, const c64* b, c64* c, int ndim, const size_t* shape,            \
+                              const ssize_t* as, const ssize_t* bs, hipStream_t st) {                      \
+    launch_binary<F, c64>(a, b, c, ndim, shape, as, bs, st, F{});                                          \
+  }                                                                                                         \
+  void musapy_##NAME##_c128_v2(const c128* a, const c128* b, c128* c, int ndim, const size_t* shape,        \
+                               const ssize_t* as, const ssize_t* bs, hipStream_t st) {                     \
+    launch_binary<F, c128>(a, b, c, ndim, shape, as, bs, st, F{});                                         \
+  }
+MPY_BINARY_C(add, CAddF)
+MPY_BINARY_C(sub, CSubF)
+MPY_BINARY_C(mul, CMulF)
+MPY_BINARY_C(div, CDivF)
+#undef MPY_BINARY_C
+void musapy_neg_c64_v2(const c64* a, c64* c, int ndim, const size_t* shape, const ssize_t* as, hipStream_t st) {
+  launch_unary<CNegF, c64, c64>(a, c, ndim, shape, as, st, CNegF{});
+}
+void musapy_neg_c128_v2(const c128* a, c128* c, int ndim, const size_t* shape, const ssize_t* as, hipStream_t st) {
+  launch_unary<CNegF, c128, c128>(a, c, ndim, shape, as, st, CNegF{});
+}
+void musapy_abs_c64_v2(const c64* a, float* c, int ndim, const size_t* shape, const ssize_t* as, hipStream_t st) {
+  launch_unary<CAbsF, float, c64>(a, c, ndim, shape, as, st, CAbsF{});
+}
+void musapy_abs_c128_v2(const c128* a, double* c, int ndim, const size_t* shape, const ssize_t* as,
+                        hipStream_t st) {
+  launch_unary<CAbsF, double, c128>(a, c, ndim, shape, as, st, CAbsF{});
+}
+
 #define MPY_UNARY(NAME, F)                                                                                  \
   void musapy_##NAME##_f32_v2(const float* a, float* c, int ndim, const size_t* shape, const ssize_t* as,   \
                               hipStream_t st) {                                                             \
@@ -723,6 +784,12 @@ MPY_CAST(f32, float, f64, double)
 MPY_CAST_FROM_INTS(i64, int64_t)
 MPY_CAST(f32, float, i64, int64_t)
 MPY_CAST(f64, double, i64, int64_t)
+// real -> complex and c64 -> c128 (kernels.rs:119-124)
+MPY_CAST(f32, float, c64, c64)
+MPY_CAST(f32, float, c128, c128)
+MPY_CAST(f64, double, c64, c64)
+MPY_CAST(f64, double, c128, c128)
+MPY_CAST(c64, c64, c128, c128)
 #undef MPY_CAST_FROM_INTS
 #undef MPY_CAST
 

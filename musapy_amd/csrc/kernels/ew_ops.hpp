@@ -5,11 +5,15 @@
 //   unary   cpu_unary_elementwise  op_builder.rs:1868-1896 (sign: v>0 -> 1, v<0 -> -1, else +0)
 //   clamp   cpu_clamp_typed        op_builder.rs:2017-2047 (v<lo ? lo : v>hi ? hi : v; NaN passes)
 //   cast    cpu_cast_pair!         op_builder.rs:227-243   (Rust `as`)
+//   compare cpu_compare_typed/_cplx op_builder.rs:1786-1864
+//   complex cpu_binary_cplx / cpu_unary_cplx_abs / cpu_cast_cplx  op_builder.rs:1652-1969, 2099-2167
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+
+#include "../../../include/musapy_kernels.h"
 
 namespace mpy {
 
@@ -21,6 +25,75 @@ struct DivF { template <class T> __device__ T operator()(T a, T b) const { retur
 struct PowF {
   __device__ float operator()(float a, float b) const { return powf(a, b); }
   __device__ double operator()(double a, double b) const { return pow(a, b); }
+};
+
+// ---- comparisons: 0/1 bytes (cpu_compare_typed / cpu_compare_cplx, op_builder.rs:1786-1864) ----
+// IEEE comparisons: a NaN operand makes every comparison false except !=, and +0 == -0.
+struct EqF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a == b; } };
+struct NeF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a != b; } };
+struct LtF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a < b; } };
+struct GtF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a > b; } };
+struct LeF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a <= b; } };
+struct GeF { template <class T> __device__ uint8_t operator()(T a, T b) const { return a >= b; } };
+// complex: equal when both parts are equal
+struct CEqF {
+  template <class C> __device__ uint8_t operator()(C a, C b) const { return a.re == b.re && a.im == b.im; }
+};
+struct CNeF {
+  template <class C> __device__ uint8_t operator()(C a, C b) const { return a.re != b.re || a.im != b.im; }
+};
+
+// ---- complex arithmetic (cpu_binary_cplx, op_builder.rs:1652-1731) ----
+// Both widths evaluate the textbook component formulas in f64 (no fma contraction) and c64
+// narrows each component to f32 once at the end, as the reference's CPU path does through
+// CplxScalar::cplx_re/cplx_from_parts; division scales by |b|^2 without Smith's rescaling.
+struct CParts {
+  double re, im;
+};
+__device__ inline CParts cparts(musapy_c64_t v) { return CParts{double(v.re), double(v.im)}; }
+__device__ inline CParts cparts(musapy_c128_t v) { return CParts{v.re, v.im}; }
+template <class C> __device__ inline C cfrom(double re, double im);
+template <> __device__ inline musapy_c64_t cfrom<musapy_c64_t>(double re, double im) {
+  return musapy_c64_t{float(re), float(im)};
+}
+template <> __device__ inline musapy_c128_t cfrom<musapy_c128_t>(double re, double im) {
+  return musapy_c128_t{re, im};
+}
+struct CAddF {
+  template <class C> __device__ C operator()(C a, C b) const {
+    CParts x = cparts(a), y = cparts(b);
+    return cfrom<C>(x.re + y.re, x.im + y.im);
+  }
+};
+struct CSubF {
+  template <class C> __device__ C operator()(C a, C b) const {
+    CParts x = cparts(a), y = cparts(b);
+    return cfrom<C>(x.re - y.re, x.im - y.im);
+  }
+};
+struct CMulF {
+  template <class C> __device__ C operator()(C a, C b) const {
+    CParts x = cparts(a), y = cparts(b);
+    return cfrom<C>(x.re * y.re - x.im * y.im, x.re * y.im + x.im * y.re);
+  }
+};
+struct CDivF {
+  template <class C> __device__ C operator()(C a, C b) const {
+    CParts x = cparts(a), y = cparts(b);
+    double den = y.re * y.re + y.im * y.im;
+    return cfrom<C>((x.re * y.re + x.im * y.im) / den, (x.im * y.re - x.re * y.im) / den);
+  }
+};
+struct CNegF {
+  template <class C> __device__ C operator()(C v) const { return C{-v.re, -v.im}; }
+};
+// |z| = sqrt(re^2 + im^2) in f64, narrowed for c64 (cpu_unary_cplx_abs, op_builder.rs:1944-1969)
+struct CAbsF {
+  __device__ float operator()(musapy_c64_t v) const {
+    CParts x = cparts(v);
+    return float(sqrt(x.re * x.re + x.im * x.im));
+  }
+  __device__ double operator()(musapy_c128_t v) const { return sqrt(v.re * v.re + v.im * v.im); }
 };
 
 // ---- unary ----
@@ -78,6 +151,17 @@ template <> struct CastF<float, int64_t> {
 };
 template <> struct CastF<double, int64_t> {
   __device__ int64_t operator()(double v) const { return sat_to_i64(v); }
+};
+// real -> complex: re = src (through f64), im = +0 (cpu_cast_cplx, op_builder.rs:2127-2167);
+// c64 -> c128 widens each component exactly (cpu_cast_c64_c128, op_builder.rs:2099-2125)
+template <class S> struct CastF<S, musapy_c64_t> {
+  __device__ musapy_c64_t operator()(S v) const { return musapy_c64_t{float(double(v)), 0.0f}; }
+};
+template <class S> struct CastF<S, musapy_c128_t> {
+  __device__ musapy_c128_t operator()(S v) const { return musapy_c128_t{double(v), 0.0}; }
+};
+template <> struct CastF<musapy_c64_t, musapy_c128_t> {
+  __device__ musapy_c128_t operator()(musapy_c64_t v) const { return musapy_c128_t{double(v.re), double(v.im)}; }
 };
 
 // f32 -> bfloat16 bits, round to nearest even.  NaN keeps sign and leading payload, quiet bit set.

@@ -137,21 +137,25 @@ void validate_cast_pair(Dtype src, Dtype dst) {
     case Dtype::Float32: case Dtype::Float64:
       break;
     case Dtype::Complex64: case Dtype::Complex128:
+      // only the c64 -> c128 widening; complex -> real has no kernel
+      if (src == Dtype::Complex64 && dst == Dtype::Complex128) return;
       throw DtypeError(std::string("cast: ") + dtype_name(src) + " -> " + dtype_name(dst) +
-                       " not supported (complex casts are outside this backend's path)");
+                       " not supported (complex -> real has no cast kernel)");
     default:
       throw DtypeError(std::string("cast: source dtype ") + dtype_name(src) +
                        " not supported (bool/float16/bfloat16 sources have no cast kernel)");
   }
   switch (dst) {
-    case Dtype::Float32: case Dtype::Float64: case Dtype::Int64: break;
-    case Dtype::Complex64: case Dtype::Complex128:
-      throw DtypeError(std::string("cast: ") + dtype_name(src) + " -> " + dtype_name(dst) +
-                       " not supported (real->complex casts are outside this backend's path)");
+    case Dtype::Float32: case Dtype::Float64: case Dtype::Int64: case Dtype::Complex64: case Dtype::Complex128:
+      break;
     default:
       throw DtypeError(std::string("cast: target dtype ") + dtype_name(dst) +
-                       " not supported (only float32/float64/int64, and float16/bfloat16 from float32)");
+                       " not supported (only float32/float64/int64/complex64/complex128, and float16/bfloat16 "
+                       "from float32)");
   }
+  if (is_complex(dst) && src != Dtype::Float32 && src != Dtype::Float64)
+    throw DtypeError(std::string("cast: ") + dtype_name(src) + " -> " + dtype_name(dst) +
+                     " not supported (complex targets take float32/float64 sources and the c64 -> c128 widening)");
   if (src == dst) throw DtypeError(std::string("cast: source and target dtype are identical (") + dtype_name(src) + ")");
 }
 
@@ -202,6 +206,19 @@ void launch_cast(const void* a, void* c, const Shape& shape, const Strides& st, 
       CAST_CASE(Uint64, uint64_t, musapy_cast_u64_i64_v2, int64_t)
       CAST_CASE(Float32, float, musapy_cast_f32_i64_v2, int64_t)
       CAST_CASE(Float64, double, musapy_cast_f64_i64_v2, int64_t)
+      default: throw DtypeError("cast pair not validated");
+    }
+  } else if (dst == Dtype::Complex64) {
+    switch (src) {
+      CAST_CASE(Float32, float, musapy_cast_f32_c64_v2, musapy_c64_t)
+      CAST_CASE(Float64, double, musapy_cast_f64_c64_v2, musapy_c64_t)
+      default: throw DtypeError("cast pair not validated");
+    }
+  } else if (dst == Dtype::Complex128) {
+    switch (src) {
+      CAST_CASE(Float32, float, musapy_cast_f32_c128_v2, musapy_c128_t)
+      CAST_CASE(Float64, double, musapy_cast_f64_c128_v2, musapy_c128_t)
+      CAST_CASE(Complex64, musapy_c64_t, musapy_cast_c64_c128_v2, musapy_c128_t)
       default: throw DtypeError("cast pair not validated");
     }
   } else if (dst == Dtype::Bfloat16 && src == Dtype::Float32) {
@@ -256,12 +273,12 @@ Array binary_elementwise(const Array& a, const Array& b, const Array* out, Binar
                       std::to_string(b.device));
   Shape out_shape = broadcast_shape({a.shape(), b.shape()});
   Dtype dt = promote(a.dtype, b.dtype, /*all_gpu=*/true);
-  if (dt != Dtype::Float32 && dt != Dtype::Float64) {
-    if (is_complex(dt))
-      throw DtypeError(std::string(op) + ": complex elementwise arithmetic is outside this backend's path");
+  if (is_complex(dt) && k == BinaryKernel::Pow)
+    throw DtypeError(std::string(op) + ": pow not supported for complex dtype " + dtype_name(dt) +
+                     " (complex scope: add/sub/mul/div)");
+  if (dt != Dtype::Float32 && dt != Dtype::Float64 && !is_complex(dt))
     throw DtypeError(std::string(op) + ": promoted dtype " + dtype_name(dt) +
-                     " not supported (compute whitelist: float32/float64)");
-  }
+                     " not supported (compute whitelist: float32/float64/complex64/complex128)");
   check_out(op, out, out_shape, dt, a, "broadcast output shape", "promoted dtype");
   StreamPtr s = pick_stream(a, out);
   if ((a.dtype != dt || b.dtype != dt) && a.shape() == out_shape && b.shape() == out_shape &&
@@ -302,8 +319,89 @@ Array binary_elementwise(const Array& a, const Array& b, const Array* out, Binar
     fn((const T*)aw.data_ptr(), (const T*)bw.data_ptr(), (T*)r.data_ptr(), nd, out_shape.data(), as.data(), \
        bs.data(), s->raw());                                                                                \
   }
-    if (dt == Dtype::Float32) BIN(float, f32) else BIN(double, f64)
+#define BINC(T, SFX)                                                                                        \
+  {                                                                                                         \
+    auto fn = k == BinaryKernel::Add ? musapy_add_##SFX##_v2                                                \
+              : k == BinaryKernel::Sub ? musapy_sub_##SFX##_v2                                              \
+              : k == BinaryKernel::Mul ? musapy_mul_##SFX##_v2                                              \
+                                       : musapy_div_##SFX##_v2;                                             \
+    fn((const T*)aw.data_ptr(), (const T*)bw.data_ptr(), (T*)r.data_ptr(), nd, out_shape.data(), as.data(), \
+       bs.data(), s->raw());                                                                                \
+  }
+    switch (dt) {
+      case Dtype::Float32: BIN(float, f32) break;
+      case Dtype::Float64: BIN(double, f64) break;
+      case Dtype::Complex64: BINC(musapy_c64_t, c64) break;
+      default: BINC(musapy_c128_t, c128) break;
+    }
 #undef BIN
+#undef BINC
+    check_launch(op);
+  }
+  aw.data->record_read(s);
+  bw.data->record_read(s);
+  r.data->record_write(s);
+  return r;
+}
+
+// op_builder.rs:1338-1557.  Promotion only picks the kernel; the output is bool.  Complex inputs
+// take eq/ne only (no total order).  Mixed dtypes are cast to the promoted dtype first, as in
+// the reference (op_builder.rs:1430-1438).
+Array comparison_elementwise(const Array& a, const Array& b, const Array* out, CompareKernel k) {
+  static const char* names[] = {"eq", "ne", "lt", "gt", "le", "ge"};
+  const char* op = names[int(k)];
+  if (a.device != b.device)
+    throw DeviceError(std::string(op) + ": device mismatch hip:" + std::to_string(a.device) + " vs hip:" +
+                      std::to_string(b.device));
+  Shape out_shape = broadcast_shape({a.shape(), b.shape()});
+  Dtype dt = promote(a.dtype, b.dtype, /*all_gpu=*/true);
+  const bool eq_ne = k == CompareKernel::Eq || k == CompareKernel::Ne;
+  if (is_complex(dt) && !eq_ne)
+    throw DtypeError(std::string(op) + ": " + op + " not supported for complex dtype " + dtype_name(dt) +
+                     " (complex has no total order; only eq/ne)");
+  if (dt != Dtype::Float32 && dt != Dtype::Float64 && !is_complex(dt))
+    throw DtypeError(std::string(op) + ": promoted dtype " + dtype_name(dt) +
+                     " not supported (compute whitelist: float32/float64, complex eq/ne)");
+  check_out(op, out, out_shape, Dtype::Bool, a, "broadcast output shape", "comparison output dtype");
+  StreamPtr s = pick_stream(a, out);
+  std::optional<Array> ac, bc;
+  if (a.dtype != dt) ac = cast_array(a, dt, s);
+  if (b.dtype != dt) bc = cast_array(b, dt, s);
+  const Array& aw = ac ? *ac : a;
+  const Array& bw = bc ? *bc : b;
+  Array r = make_output(out, out_shape, Dtype::Bool, a.device, s, {&aw, &bw});
+  aw.data->wait_last_write_on(s);
+  bw.data->wait_last_write_on(s);
+  if (shape_numel(out_shape) > 0) {
+    Strides as = aw.shape() == out_shape ? aw.layout.strides : broadcast_strides(aw.layout, out_shape);
+    Strides bs = bw.shape() == out_shape ? bw.layout.strides : broadcast_strides(bw.layout, out_shape);
+    const int nd = int(out_shape.size());
+    uint8_t* c = (uint8_t*)r.data_ptr();
+#define CMP(T, SFX)                                                                                       \
+  {                                                                                                       \
+    auto fn = k == CompareKernel::Eq   ? musapy_eq_##SFX##_v2                                             \
+              : k == CompareKernel::Ne ? musapy_ne_##SFX##_v2                                             \
+              : k == CompareKernel::Lt ? musapy_lt_##SFX##_v2                                             \
+              : k == CompareKernel::Gt ? musapy_gt_##SFX##_v2                                             \
+              : k == CompareKernel::Le ? musapy_le_##SFX##_v2                                             \
+                                       : musapy_ge_##SFX##_v2;                                            \
+    fn((const T*)aw.data_ptr(), (const T*)bw.data_ptr(), c, nd, out_shape.data(), as.data(), bs.data(), \
+       s->raw());                                                                                         \
+  }
+#define CMPC(T, SFX)                                                                                      \
+  {                                                                                                       \
+    auto fn = k == CompareKernel::Eq ? musapy_eq_##SFX##_v2 : musapy_ne_##SFX##_v2;                       \
+    fn((const T*)aw.data_ptr(), (const T*)bw.data_ptr(), c, nd, out_shape.data(), as.data(), bs.data(), \
+       s->raw());                                                                                         \
+  }
+    switch (dt) {
+      case Dtype::Float32: CMP(float, f32) break;
+      case Dtype::Float64: CMP(double, f64) break;
+      case Dtype::Complex64: CMPC(musapy_c64_t, c64) break;
+      default: CMPC(musapy_c128_t, c128) break;
+    }
+#undef CMP
+#undef CMPC
     check_launch(op);
   }
   aw.data->record_read(s);
@@ -315,16 +413,40 @@ Array binary_elementwise(const Array& a, const Array& b, const Array* out, Binar
 Array unary_elementwise(const Array& a, const Array* out, UnaryKernel k) {
   const char* op = uname(k);
   Dtype dt = a.dtype;
-  if (dt != Dtype::Float32 && dt != Dtype::Float64) {
-    if (is_complex(dt))
-      throw DtypeError(std::string(op) + ": complex elementwise ops are outside this backend's path");
-    throw DtypeError(std::string(op) + ": dtype " + dtype_name(dt) + " not supported (only float32/float64)");
+  if (is_complex(dt)) {
+    if (k != UnaryKernel::Neg && k != UnaryKernel::Abs)
+      throw DtypeError(std::string(op) + ": " + op + " not supported for complex dtype " + dtype_name(dt) +
+                       " (complex scope: neg/abs)");
+  } else if (dt != Dtype::Float32 && dt != Dtype::Float64) {
+    throw DtypeError(std::string(op) + ": dtype " + dtype_name(dt) +
+                     " not supported (only float32/float64/complex64/complex128)");
   }
-  check_out(op, out, a.shape(), dt, a, "input shape", "expected output dtype");
+  // abs of a complex array is real (op_builder.rs:585-589)
+  Dtype odt = !(is_complex(dt) && k == UnaryKernel::Abs) ? dt
+              : dt == Dtype::Complex64                      ? Dtype::Float32
+                                                            : Dtype::Float64;
+  check_out(op, out, a.shape(), odt, a, "input shape", "expected output dtype");
   StreamPtr s = pick_stream(a, out);
-  Array r = make_output(out, a.shape(), dt, a.device, s, {&a});
+  Array r = make_output(out, a.shape(), odt, a.device, s, {&a});
   a.data->wait_last_write_on(s);
-  if (a.size() > 0) {
+  if (a.size() > 0 && is_complex(dt)) {
+    const int nd = int(a.ndim());
+    const size_t* sh = a.shape().data();
+    const ssize_t* st = a.layout.strides.data();
+    if (dt == Dtype::Complex64) {
+      if (k == UnaryKernel::Abs)
+        musapy_abs_c64_v2((const musapy_c64_t*)a.data_ptr(), (float*)r.data_ptr(), nd, sh, st, s->raw());
+      else
+        musapy_neg_c64_v2((const musapy_c64_t*)a.data_ptr(), (musapy_c64_t*)r.data_ptr(), nd, sh, st, s->raw());
+    } else {
+      if (k == UnaryKernel::Abs)
+        musapy_abs_c128_v2((const musapy_c128_t*)a.data_ptr(), (double*)r.data_ptr(), nd, sh, st, s->raw());
+      else
+        musapy_neg_c128_v2((const musapy_c128_t*)a.data_ptr(), (musapy_c128_t*)r.data_ptr(), nd, sh, st,
+                           s->raw());
+    }
+    check_launch(op);
+  } else if (a.size() > 0) {
     const int nd = int(a.ndim());
 #define UN(T, SFX)                                                                                               \
   {                                                                                                              \

@@ -17,6 +17,7 @@ namespace ops {
 enum class BinaryKernel { Add, Sub, Mul, Div, Pow };
 enum class UnaryKernel { Sin, Cos, Exp, Log, Abs, Sign, Neg };
 enum class ReduceKernel { Sum, Prod, Max, Min, Mean, Argmax, Argmin };
+enum class CompareKernel { Eq, Ne, Lt, Gt, Le, Ge };
 
 // broadcast.rs:24-92
 Shape broadcast_shape(const std::vector<Shape>& shapes);
@@ -24,6 +25,8 @@ Strides broadcast_strides(const Layout& layout, const Shape& target);
 
 // op_builder.rs:315 / 550 / 740 / 1055 / 1130
 Array binary_elementwise(const Array& a, const Array& b, const Array* out, BinaryKernel k);
+// op_builder.rs:1338-1557: output dtype is always bool (one 0/1 byte per element)
+Array comparison_elementwise(const Array& a, const Array& b, const Array* out, CompareKernel k);
 Array unary_elementwise(const Array& a, const Array* out, UnaryKernel k);
 Array clamp_elementwise(const Array& a, double lo, double hi, const Array* out);
 Array cast_array(const Array& a, Dtype target, const StreamPtr& stream);

@@ -9,7 +9,9 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <cctype>
 #include <cstring>
+#include <optional>
 
 #include "../kernels/plan.hpp"
 #include "../ops/ops.hpp"
@@ -36,6 +38,35 @@ int parse_device(const py::object& dev) {
   if (s == "cpu")
     throw DeviceError("device 'cpu': this backend runs the path on the GPU only (no host compute path)");
   throw DeviceError("invalid device string '" + s + "' (expected 'hip:N')");
+}
+
+// ---- dtype objects (rust/musapy-python/src/dtype.rs:21-190) ----
+struct PyDtype {
+  Dtype d;
+};
+
+// parse_dtype (dtype.rs:44-63): short aliases, full names and the compatibility names,
+// case-insensitive.
+std::optional<Dtype> dtype_from_name(std::string s) {
+  for (char& ch : s) ch = char(std::tolower((unsigned char)ch));
+  if (s == "b1" || s == "bool8") return Dtype::Bool;
+  if (s == "half") return Dtype::Float16;
+  if (s == "single") return Dtype::Float32;
+  if (s == "double") return Dtype::Float64;
+  for (int i = 0; i <= int(Dtype::Complex128); ++i)
+    if (s == dtype_name(Dtype(i)) || s == dtype_short(Dtype(i))) return Dtype(i);
+  return std::nullopt;
+}
+
+// dtype argument extraction (dtype.rs:73-95): a Dtype instance or a dtype string.
+Dtype dtype_arg(const py::handle& o) {
+  if (py::isinstance<PyDtype>(o)) return o.cast<const PyDtype&>().d;
+  if (py::isinstance<py::str>(o)) {
+    std::string s = o.cast<std::string>();
+    if (auto d = dtype_from_name(s)) return *d;
+    throw py::value_error("unknown dtype: " + s);
+  }
+  throw py::type_error("dtype must be a Dtype instance or a dtype string (e.g. 'f32', 'float32')");
 }
 
 py::tuple to_tuple(const std::vector<size_t>& v) {
@@ -179,12 +210,49 @@ PYBIND11_MODULE(_core, m) {
     return py::cast(default_stream(g_default_device));
   });
 
+  py::class_<PyDtype>(m, "Dtype")
+      .def(py::init([](const std::string& name) {
+             auto d = dtype_from_name(name);
+             if (!d) throw py::value_error("unknown dtype: " + name);
+             return PyDtype{*d};
+           }),
+           py::arg("name"))
+      .def("__repr__", [](const PyDtype& t) { return std::string(dtype_name(t.d)); })
+      .def("__str__", [](const PyDtype& t) { return std::string(dtype_name(t.d)); })
+      .def("__format__", [](const PyDtype& t, const std::string&) { return std::string(dtype_name(t.d)); })
+      .def_property_readonly("name", [](const PyDtype& t) { return std::string(dtype_name(t.d)); })
+      .def_property_readonly("element_size", [](const PyDtype& t) { return element_size(t.d); })
+      .def_property_readonly("is_floating", [](const PyDtype& t) { return dtype_category(t.d) == 3; })
+      .def_property_readonly("is_integer", [](const PyDtype& t) { return dtype_category(t.d) <= 2; })
+      .def_property_readonly("is_complex", [](const PyDtype& t) { return is_complex(t.d); })
+      .def("__eq__",
+           [](const PyDtype& t, const py::object& o) {
+             if (py::isinstance<PyDtype>(o)) return o.cast<const PyDtype&>().d == t.d;
+             if (py::isinstance<py::str>(o)) {
+               auto d = dtype_from_name(o.cast<std::string>());
+               return d && *d == t.d;
+             }
+             return false;
+           })
+      .def("__ne__",
+           [](const PyDtype& t, const py::object& o) {
+             if (py::isinstance<PyDtype>(o)) return o.cast<const PyDtype&>().d != t.d;
+             if (py::isinstance<py::str>(o)) {
+               auto d = dtype_from_name(o.cast<std::string>());
+               return !(d && *d == t.d);
+             }
+             return true;
+           })
+      .def("__hash__", [](const PyDtype& t) { return py::hash(py::str(dtype_name(t.d))); });
+  // dtype constants (dtype.rs:171-190)
+  for (int i = 0; i <= int(Dtype::Complex128); ++i) m.attr(dtype_name(Dtype(i))) = PyDtype{Dtype(i)};
+
   py::class_<Array>(m, "Array")
       .def_property_readonly("stream", [](const Array& a) { return a.stream; })
       .def_property_readonly("shape", [](const Array& a) { return to_tuple(a.shape()); })
       .def_property_readonly("ndim", [](const Array& a) { return a.ndim(); })
       .def_property_readonly("size", [](const Array& a) { return a.size(); })
-      .def_property_readonly("dtype", [](const Array& a) { return std::string(dtype_short(a.dtype)); })
+      .def_property_readonly("dtype", [](const Array& a) { return PyDtype{a.dtype}; })
       .def_property_readonly("device", [](const Array& a) { return dev_str(a.device); })
       .def_property_readonly("nbytes", [](const Array& a) { return a.nbytes(); })
       .def_property_readonly("strides", [](const Array& a) { return a.layout.strides; })
@@ -202,7 +270,21 @@ PYBIND11_MODULE(_core, m) {
       .def("__pow__", [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Pow); })
       .def("__neg__", [](const Array& a) { return unary_elementwise(a, nullptr, UnaryKernel::Neg); })
       .def("__abs__", [](const Array& a) { return unary_elementwise(a, nullptr, UnaryKernel::Abs); })
-      .def("astype", [](const Array& a, const std::string& d) { return astype_op(a, parse_dtype(d), nullptr); });
+      // comparisons (rust/musapy-python/src/array.rs:174-208): elementwise, bool result
+      .def("__eq__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Eq); },
+           py::is_operator())
+      .def("__ne__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Ne); },
+           py::is_operator())
+      .def("__lt__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Lt); },
+           py::is_operator())
+      .def("__gt__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Gt); },
+           py::is_operator())
+      .def("__le__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Le); },
+           py::is_operator())
+      .def("__ge__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Ge); },
+           py::is_operator())
+      .def("astype", [](const Array& a, const py::object& d) { return astype_op(a, dtype_arg(d), nullptr); },
+           py::arg("dtype"));
 
 #define BIN(NAME, K)                                                                                 \
   m.def(                                                                                             \
@@ -214,6 +296,17 @@ PYBIND11_MODULE(_core, m) {
   BIN(div, BinaryKernel::Div)
   BIN(pow, BinaryKernel::Pow)
 #undef BIN
+#define CMP(NAME, K)                                                                                          \
+  m.def(                                                                                                      \
+      #NAME, [](const Array& a, const Array& b, const Array* out) { return comparison_elementwise(a, b, out, K); }, \
+      py::arg("a"), py::arg("b"), py::arg("out") = nullptr);
+  CMP(eq, CompareKernel::Eq)
+  CMP(ne, CompareKernel::Ne)
+  CMP(lt, CompareKernel::Lt)
+  CMP(gt, CompareKernel::Gt)
+  CMP(le, CompareKernel::Le)
+  CMP(ge, CompareKernel::Ge)
+#undef CMP
 #define UN(NAME, K) \
   m.def(#NAME, [](const Array& a, const Array* out) { return unary_elementwise(a, out, K); }, py::arg("a"), \
         py::arg("out") = nullptr);
@@ -227,7 +320,7 @@ PYBIND11_MODULE(_core, m) {
 #undef UN
   m.def("clamp", [](const Array& a, double lo, double hi, const Array* out) { return clamp_elementwise(a, lo, hi, out); },
         py::arg("a"), py::arg("lo"), py::arg("hi"), py::arg("out") = nullptr);
-  m.def("astype", [](const Array& a, const std::string& d, const Array* out) { return astype_op(a, parse_dtype(d), out); },
+  m.def("astype", [](const Array& a, const py::object& d, const Array* out) { return astype_op(a, dtype_arg(d), out); },
         py::arg("a"), py::arg("dtype"), py::arg("out") = nullptr);
 
 #define RED(NAME, K)                                                                                      \

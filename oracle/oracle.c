@@ -9,6 +9,12 @@
  *   oracle_binary_*        cpu_binary_typed/_op     op_builder.rs:1618-1626, 1734-1760
  *   oracle_unary_*         cpu_unary_elementwise    op_builder.rs:1868-1896, 1971-1993
  *   oracle_clamp_*         cpu_clamp_typed          op_builder.rs:2004-2047
+ *   oracle_compare         cpu_comparison_elementwise / cpu_compare_typed / cpu_compare_cplx
+ *                                                   op_builder.rs:1765-1864 (PartialEq/PartialOrd)
+ *   oracle_binary_cplx     cpu_binary_cplx          op_builder.rs:1652-1731 (components in f64)
+ *   oracle_unary_cplx      cpu_unary_elementwise complex arms + cpu_unary_cplx_abs
+ *                                                   op_builder.rs:1904-1969
+ *   oracle_cast (complex)  cpu_cast_cplx / cpu_cast_c64_c128  op_builder.rs:2080-2167
  *   oracle_cast            cpu_cast + cpu_cast_pair op_builder.rs:227-243, 2052-2097 (Rust `as`)
  *   oracle_reduce          cpu_reduce_offset/typed  op_builder.rs:3368-3394, 3496-3582
  *                          cpu_mean_typed           op_builder.rs:3585-3619
@@ -75,6 +81,113 @@ void oracle_binary_f64(int op, const double* a, const double* b, double* c, int 
       default: r = pow(x, y); break;
     }
     c[i] = r;
+  }
+}
+
+/* ---- complex elementwise: interleaved (re, im); CplxScalar reads both widths as f64 and
+ * cplx_from_parts narrows with `as f32` (op_builder.rs:1655-1687) ---- */
+static void cplx_load(int dtype, const void* p, int64_t off, double* re, double* im) {
+  if (dtype == ORACLE_C64) {
+    *re = ((const float*)p)[2 * off];
+    *im = ((const float*)p)[2 * off + 1];
+  } else {
+    *re = ((const double*)p)[2 * off];
+    *im = ((const double*)p)[2 * off + 1];
+  }
+}
+
+static void cplx_store(int dtype, void* p, size_t i, double re, double im) {
+  if (dtype == ORACLE_C64) {
+    ((float*)p)[2 * i] = (float)re;
+    ((float*)p)[2 * i + 1] = (float)im;
+  } else {
+    ((double*)p)[2 * i] = re;
+    ((double*)p)[2 * i + 1] = im;
+  }
+}
+
+void oracle_binary_cplx(int op, int dtype, const void* a, const void* b, void* c, int ndim, const size_t* shape,
+                        const int64_t* as, const int64_t* bs) {
+  size_t n = numel(shape, ndim);
+  for (size_t i = 0; i < n; ++i) {
+    double ar, ai, br, bi, re, im;
+    cplx_load(dtype, a, oracle_offset_nd(i, shape, as, ndim), &ar, &ai);
+    cplx_load(dtype, b, oracle_offset_nd(i, shape, bs, ndim), &br, &bi);
+    switch (op) {
+      case ORACLE_ADD: re = ar + br; im = ai + bi; break;
+      case ORACLE_SUB: re = ar - br; im = ai - bi; break;
+      case ORACLE_MUL: re = ar * br - ai * bi; im = ar * bi + ai * br; break;
+      default: { /* ORACLE_DIV */
+        double den = br * br + bi * bi;
+        re = (ar * br + ai * bi) / den;
+        im = (ai * br - ar * bi) / den;
+      }
+    }
+    cplx_store(dtype, c, i, re, im);
+  }
+}
+
+/* op: ORACLE_NEG (complex output) or ORACLE_ABS (real output: f32 for c64, f64 for c128) */
+void oracle_unary_cplx(int op, int dtype, const void* a, void* c, int ndim, const size_t* shape,
+                       const int64_t* as) {
+  size_t n = numel(shape, ndim);
+  for (size_t i = 0; i < n; ++i) {
+    int64_t off = oracle_offset_nd(i, shape, as, ndim);
+    if (op == ORACLE_NEG) {
+      /* the reference negates the stored components directly (no f64 round trip) */
+      if (dtype == ORACLE_C64) {
+        ((float*)c)[2 * i] = -((const float*)a)[2 * off];
+        ((float*)c)[2 * i + 1] = -((const float*)a)[2 * off + 1];
+      } else {
+        ((double*)c)[2 * i] = -((const double*)a)[2 * off];
+        ((double*)c)[2 * i + 1] = -((const double*)a)[2 * off + 1];
+      }
+    } else {
+      double re, im;
+      cplx_load(dtype, a, off, &re, &im);
+      double r = sqrt(re * re + im * im);
+      if (dtype == ORACLE_C64) ((float*)c)[i] = (float)r;
+      else ((double*)c)[i] = r;
+    }
+  }
+}
+
+/* ---- comparisons: one 0/1 byte per element (op_builder.rs:1765-1864) ---- */
+static int cmp_real(int op, double x, double y) {
+  switch (op) {
+    case ORACLE_EQ: return x == y;
+    case ORACLE_NE: return x != y;
+    case ORACLE_LT: return x < y;
+    case ORACLE_GT: return x > y;
+    case ORACLE_LE: return x <= y;
+    default: return x >= y;
+  }
+}
+
+void oracle_compare(int op, int dtype, const void* a, const void* b, uint8_t* c, int ndim, const size_t* shape,
+                    const int64_t* as, const int64_t* bs) {
+  size_t n = numel(shape, ndim);
+  for (size_t i = 0; i < n; ++i) {
+    int64_t ao = oracle_offset_nd(i, shape, as, ndim), bo = oracle_offset_nd(i, shape, bs, ndim);
+    int r;
+    if (dtype == ORACLE_F32) {
+      /* f32 compared as f32: widening to double is exact, so the order and NaN rules are kept */
+      r = cmp_real(op, ((const float*)a)[ao], ((const float*)b)[bo]);
+    } else if (dtype == ORACLE_F64) {
+      r = cmp_real(op, ((const double*)a)[ao], ((const double*)b)[bo]);
+    } else {
+      double ar, ai, br, bi;
+      if (dtype == ORACLE_C64) {
+        ar = ((const float*)a)[2 * ao], ai = ((const float*)a)[2 * ao + 1];
+        br = ((const float*)b)[2 * bo], bi = ((const float*)b)[2 * bo + 1];
+      } else {
+        ar = ((const double*)a)[2 * ao], ai = ((const double*)a)[2 * ao + 1];
+        br = ((const double*)b)[2 * bo], bi = ((const double*)b)[2 * bo + 1];
+      }
+      /* complex: eq / ne only (ordering comparisons are rejected before dispatch) */
+      r = op == ORACLE_EQ ? (ar == br && ai == bi) : (ar != br || ai != bi);
+    }
+    c[i] = (uint8_t)(r ? 1 : 0);
   }
 }
 
@@ -159,6 +272,19 @@ static double load_as_f64(int t, const void* p, int64_t off, int* is_int, int64_
 
 void oracle_cast(int src, int dst, const void* a, void* c, int ndim, const size_t* shape, const int64_t* as) {
   size_t n = numel(shape, ndim);
+  if (dst == ORACLE_C64 || dst == ORACLE_C128) {
+    /* real -> complex: re = src as f64 then narrowed by cplx_from_parts, im = +0;
+     * c64 -> c128: each component widened */
+    for (size_t i = 0; i < n; ++i) {
+      int64_t off = oracle_offset_nd(i, shape, as, ndim);
+      double re, im = 0.0;
+      if (src == ORACLE_C64) cplx_load(src, a, off, &re, &im);
+      else if (src == ORACLE_F32) re = ((const float*)a)[off];
+      else re = ((const double*)a)[off];
+      cplx_store(dst, c, i, re, im);
+    }
+    return;
+  }
   for (size_t i = 0; i < n; ++i) {
     int64_t off = oracle_offset_nd(i, shape, as, ndim);
     int kind;

@@ -9,6 +9,7 @@ array that lives on the accelerator device (so promotion uses the GPU-narrow rul
   promote                rust/musapy-core/src/dtype.rs:206-334
   broadcast shape/strides rust/musapy-ops/src/broadcast.rs:24-92
   binary/unary/clamp     rust/musapy-ops/src/op_builder.rs:315-532, 550-732, 740-891
+  comparisons            op_builder.rs:1338-1557 (output bool; complex eq/ne only)
   cast validation        op_builder.rs:904-962 (+ the new f32 -> f16/bf16 pairs)
   reduction_axis         op_builder.rs:2310-3139 (compute dtype 2209-2225, axis=None -> 1-D)
   reduce_multi / arg_reduce_multi / resolve_axes   rust/musapy-ops/src/reduction.rs:21-226
@@ -26,6 +27,7 @@ _LIB = None
 
 BIN = {"add": 0, "sub": 1, "mul": 2, "div": 3, "pow": 4}
 UN = {"sin": 0, "cos": 1, "exp": 2, "log": 3, "abs": 4, "sign": 5, "neg": 6}
+CMP = {"eq": 0, "ne": 1, "lt": 2, "gt": 3, "le": 4, "ge": 5}
 RED = {"sum": 0, "prod": 1, "max": 2, "min": 3, "mean": 4, "argmax": 5, "argmin": 6}
 TCODE = {"i8": 0, "i16": 1, "i32": 2, "i64": 3, "u8": 4, "u16": 5, "u32": 6, "u64": 7, "f32": 8, "f64": 9,
          "c64": 10, "c128": 11}
@@ -141,12 +143,19 @@ def _ptr(x: np.ndarray):
 
 # ---------------------------------------------------------------------------------------------
 def validate_cast(src: str, dst: str):
+    """validate_cast_pair, op_builder.rs:904-962 (+ the new f32 -> f16/bf16 pairs)."""
     if src == "f32" and dst in ("f16", "bf16"):
         return
+    if src in ("c64", "c128"):
+        if src == "c64" and dst == "c128":
+            return
+        raise OracleError(f"cast {src} -> {dst}")
     if src not in ("i8", "i16", "i32", "i64", "u8", "u16", "u32", "u64", "f32", "f64"):
         raise OracleError(f"cast source {src}")
-    if dst not in ("f32", "f64", "i64"):
+    if dst not in ("f32", "f64", "i64", "c64", "c128"):
         raise OracleError(f"cast target {dst}")
+    if dst in ("c64", "c128") and src not in ("f32", "f64"):
+        raise OracleError(f"cast {src} -> {dst}")
     if src == dst:
         raise OracleError("identical cast")
 
@@ -170,7 +179,9 @@ def cast(x: np.ndarray, dst: str) -> np.ndarray:
 def binary(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
     shape = broadcast_shape(a.shape, b.shape)
     dt = promote(dtype_of(a), dtype_of(b), True)
-    if dt not in ("f32", "f64"):
+    if dt in ("c64", "c128") and op == "pow":
+        raise OracleError(f"{op}: complex pow")
+    if dt not in ("f32", "f64", "c64", "c128"):
         raise OracleError(f"{op}: promoted dtype {dt}")
     aw = a if dtype_of(a) == dt else cast(a, dt)
     bw = b if dtype_of(b) == dt else cast(b, dt)
@@ -178,14 +189,46 @@ def binary(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
     if out.size:
         ast = _estrides(aw) if aw.shape == shape else _bstrides(aw, shape)
         bst = _estrides(bw) if bw.shape == shape else _bstrides(bw, shape)
-        f = lib().oracle_binary_f32 if dt == "f32" else lib().oracle_binary_f64
-        f(BIN[op], _ptr(aw), _ptr(bw), _ptr(out), len(shape), _c(shape, ctypes.c_size_t),
-          _c(ast, ctypes.c_int64), _c(bst, ctypes.c_int64))
+        args = (_ptr(aw), _ptr(bw), _ptr(out), len(shape), _c(shape, ctypes.c_size_t), _c(ast, ctypes.c_int64),
+                _c(bst, ctypes.c_int64))
+        if dt in ("c64", "c128"):
+            lib().oracle_binary_cplx(BIN[op], TCODE[dt], *args)
+        else:
+            f = lib().oracle_binary_f32 if dt == "f32" else lib().oracle_binary_f64
+            f(BIN[op], *args)
     return out
+
+
+def compare(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """comparison_elementwise: promote for the kernel only, bool output (op_builder.rs:1338-1557)."""
+    shape = broadcast_shape(a.shape, b.shape)
+    dt = promote(dtype_of(a), dtype_of(b), True)
+    if dt in ("c64", "c128") and op not in ("eq", "ne"):
+        raise OracleError(f"{op}: complex ordering")
+    if dt not in ("f32", "f64", "c64", "c128"):
+        raise OracleError(f"{op}: promoted dtype {dt}")
+    aw = a if dtype_of(a) == dt else cast(a, dt)
+    bw = b if dtype_of(b) == dt else cast(b, dt)
+    out = np.zeros(shape, dtype=np.uint8)
+    if out.size:
+        ast = _estrides(aw) if aw.shape == shape else _bstrides(aw, shape)
+        bst = _estrides(bw) if bw.shape == shape else _bstrides(bw, shape)
+        lib().oracle_compare(CMP[op], TCODE[dt], _ptr(aw), _ptr(bw), _ptr(out), len(shape),
+                             _c(shape, ctypes.c_size_t), _c(ast, ctypes.c_int64), _c(bst, ctypes.c_int64))
+    return out.view(np.bool_)
 
 
 def unary(op: str, a: np.ndarray) -> np.ndarray:
     dt = dtype_of(a)
+    if dt in ("c64", "c128"):
+        if op not in ("neg", "abs"):
+            raise OracleError(f"{op}: complex")
+        odt = ("f32" if dt == "c64" else "f64") if op == "abs" else dt
+        out = np.empty(a.shape, dtype=NP[odt])
+        if out.size:
+            lib().oracle_unary_cplx(UN[op], TCODE[dt], _ptr(a), _ptr(out), a.ndim, _c(a.shape, ctypes.c_size_t),
+                                    _c(_estrides(a), ctypes.c_int64))
+        return out
     if dt not in ("f32", "f64"):
         raise OracleError(f"{op}: dtype {dt}")
     out = np.empty(a.shape, dtype=NP[dt])

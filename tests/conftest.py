@@ -40,11 +40,27 @@ def ulp_diff_f64(a, b):
     return out
 
 
-def assert_bits_equal(got, want, what=""):
+def assert_bits_equal(got, want, what="", nan_bits=False):
+    """Bit-exact comparison.  A NaN produced by an invalid operation (inf - inf, 0 * inf, ...)
+    has a platform-defined sign and payload -- x86 SSE returns the negative "default NaN",
+    CDNA the positive canonical quiet NaN -- so unless `nan_bits` is set, a NaN component
+    matches any NaN component; every other value must agree in every bit."""
     got = np.asarray(got)
     want = np.asarray(want)
     assert got.shape == want.shape, (what, got.shape, want.shape)
     assert got.dtype == want.dtype, (what, got.dtype, want.dtype)
+    if not nan_bits and (np.issubdtype(got.dtype, np.floating) or np.issubdtype(got.dtype, np.complexfloating)):
+        comp = np.float32 if got.dtype in (np.float32, np.complex64) else (
+            np.float64 if got.dtype in (np.float64, np.complex128) else got.dtype)
+        gc = np.ascontiguousarray(got).reshape(-1).view(comp)
+        wc = np.ascontiguousarray(want).reshape(-1).view(comp)
+        both_nan = np.isnan(gc) & np.isnan(wc)
+        if both_nan.any():
+            gc, wc = gc.copy(), wc.copy()
+            gc[both_nan] = 0
+            wc[both_nan] = 0
+            got = gc.view(got.dtype).reshape(got.shape)
+            want = wc.view(want.dtype).reshape(want.shape)
     size = got.dtype.itemsize
     word = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64, 16: np.uint64}[size]
     per = 2 if size == 16 else 1
