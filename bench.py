@@ -171,6 +171,16 @@ def all_config_ops(ms):
     W2 = [ms.astype(Z2[k], "c128") for k in range(K)]
     ops.append(("c128 mul 16M", lambda i: ms.mul(W[i % K], W2[i % K]), 48 * M))
     ops.append(("c128 div 16M", lambda i: ms.div(W[i % K], W2[i % K]), 48 * M))
+    # contiguous() materialisation: 2-D transpose (transpose2d entry point), 3-D permute, flip
+    ops.append(("contiguous X^T f32 (8192,8192)", lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n))
+    P = _copies(ms, np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32), K)
+    ops.append(("contiguous permute(2,0,1) f32 (8192,128,64)",
+                lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n))
+    ops.append(("contiguous flip axis=1 f32 (8192,8192)", lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n))
+    wm = (r.standard_normal((4096, 4096)) + 1j * r.standard_normal((4096, 4096))).astype(np.complex128)
+    WM = _copies(ms, wm, K)
+    ops.append(("contiguous ^T c128 (4096,4096)", lambda i: ms.contiguous(ms.transpose(WM[i % K])),
+                32 * 4096 * 4096))
     return ops
 
 

@@ -284,9 +284,15 @@ void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t*
 /* kernels.rs:322 */ void musapy_copy_f64(const double* input, double* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
 /* kernels.rs:323 */ void musapy_copy_i32(const int32_t* input, int32_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
 /* kernels.rs:324 */ void musapy_copy_i64(const int64_t* input, int64_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
-/* new: 1- and 2-byte element copies (bool/int8/uint8, int16/uint16/float16/bfloat16 views) */
+/* new: 1-, 2- and 16-byte element copies (bool/int8/uint8; int16/uint16/float16/bfloat16; complex128) */
 void musapy_copy_u8(const uint8_t* input, uint8_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
 void musapy_copy_u16(const uint16_t* input, uint16_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+void musapy_copy_c128(const musapy_c128_t* input, musapy_c128_t* output, int ndim, const size_t* shape, const ssize_t* in_strides, hipStream_t stream);
+/* 2-D transpose materialisation: src is C-contiguous (cols, rows); dst[r*cols + c] = src[c*rows + r] */
+/* kernels.rs:327 */ void musapy_copy_transpose2d_f32(const float* src, float* dst, size_t rows, size_t cols, hipStream_t stream);
+/* kernels.rs:328 */ void musapy_copy_transpose2d_f64(const double* src, double* dst, size_t rows, size_t cols, hipStream_t stream);
+/* kernels.rs:329 */ void musapy_copy_transpose2d_i32(const int32_t* src, int32_t* dst, size_t rows, size_t cols, hipStream_t stream);
+/* kernels.rs:330 */ void musapy_copy_transpose2d_i64(const int64_t* src, int64_t* dst, size_t rows, size_t cols, hipStream_t stream);
 
 /* ---- fused mixed-dtype binary (new; no counterpart in kernels.rs) ----
  * c = op(C(a), C(b)) where C(x) is the Rust `as` cast to c_dtype used by the cast kernels above:

@@ -827,6 +827,22 @@ MPY_COPY(i32, int32_t)
 MPY_COPY(i64, int64_t)
 MPY_COPY(u8, uint8_t)
 MPY_COPY(u16, uint16_t)
+MPY_COPY(c128, c128)
 #undef MPY_COPY
+
+// 2-D transpose materialisation (kernels.rs:327-330): src is a C-contiguous (cols, rows)
+// array, dst[r*cols + c] = src[c*rows + r].  This is the copy of the transposed view
+// (shape (rows, cols), strides (1, rows)), which the launcher sends to the LDS-tiled kernel.
+#define MPY_COPY_T2D(NAME, T)                                                                                \
+  void musapy_copy_transpose2d_##NAME(const T* src, T* dst, size_t rows, size_t cols, hipStream_t st) {      \
+    const size_t shape[2] = {rows, cols};                                                                    \
+    const ssize_t strides[2] = {1, ssize_t(rows)};                                                           \
+    launch_unary<IdentityF, T, T>(src, dst, 2, shape, strides, st, IdentityF{});                             \
+  }
+MPY_COPY_T2D(f32, float)
+MPY_COPY_T2D(f64, double)
+MPY_COPY_T2D(i32, int32_t)
+MPY_COPY_T2D(i64, int64_t)
+#undef MPY_COPY_T2D
 
 }  // extern "C"

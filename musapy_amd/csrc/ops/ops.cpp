@@ -3,8 +3,9 @@
 // Ports the control flow of rust/musapy-ops/src/op_builder.rs (binary_elementwise 315-532,
 // unary_elementwise 550-732, clamp_elementwise 740-891, validate_cast_pair 904-962,
 // cast_array 1055-1119, astype_op 1130-1292, reduction_axis 2310-3139, cumsum_op 3144-3363),
-// rust/musapy-ops/src/reduction.rs (axis resolution, reduce_multi, arg_reduce_multi) and
-// rust/musapy-ops/src/broadcast.rs.  Phase B only calls the C kernel ABI; there is no host
+// rust/musapy-ops/src/reduction.rs (axis resolution, reduce_multi, arg_reduce_multi),
+// rust/musapy-ops/src/broadcast.rs and rust/musapy-ops/src/indexing.rs (views, contiguous
+// 181-237 with copy_into 816-916).  Phase B only calls the C kernel ABI; there is no host
 // compute path.  Path selection for reductions differs from the reference (which switches on
 // axis_len thresholds, op_builder.rs:2513-2514): the kernel library reports how many tiles per
 // output a reduction needs to fill the GPU (musapy_reduce_tiles_hint) and the op layer uses the
@@ -15,22 +16,6 @@
 
 #include "../../../include/musapy_kernels.h"
 #include "../../../include/musapy_hip_runtime.h"
-
-extern "C" {
-// copy kernels (rust/musapy-ops/src/kernels.rs:321-324 signature; u8/u16 are new)
-void musapy_copy_f32(const float* input, float* output, int ndim, const size_t* shape, const ssize_t* in_strides,
-                     hipStream_t stream);
-void musapy_copy_f64(const double* input, double* output, int ndim, const size_t* shape, const ssize_t* in_strides,
-                     hipStream_t stream);
-void musapy_copy_i32(const int32_t* input, int32_t* output, int ndim, const size_t* shape, const ssize_t* in_strides,
-                     hipStream_t stream);
-void musapy_copy_i64(const int64_t* input, int64_t* output, int ndim, const size_t* shape,
-                     const ssize_t* in_strides, hipStream_t stream);
-void musapy_copy_u8(const uint8_t* input, uint8_t* output, int ndim, const size_t* shape, const ssize_t* in_strides,
-                    hipStream_t stream);
-void musapy_copy_u16(const uint16_t* input, uint16_t* output, int ndim, const size_t* shape,
-                     const ssize_t* in_strides, hipStream_t stream);
-}
 
 namespace mpy {
 namespace ops {
@@ -907,20 +892,21 @@ Array contiguous(const Array& a) {
     Shape sh = a.shape();
     Strides st = a.layout.strides;
     const int nd = int(sh.size());
-    switch (es) {
+    // the transposed view of a C-contiguous 2-D array takes the reference's transpose2d entry
+    // point (indexing.rs:833-838); everything else the general stride-aware copy
+    const bool t2d = nd == 2 && st[0] == 1 && st[1] == ssize_t(sh[0]);
+    if (t2d && es == 4) {
+      musapy_copy_transpose2d_i32((const int32_t*)a.data_ptr(), (int32_t*)r.data_ptr(), sh[0], sh[1], s->raw());
+    } else if (t2d && es == 8) {
+      musapy_copy_transpose2d_i64((const int64_t*)a.data_ptr(), (int64_t*)r.data_ptr(), sh[0], sh[1], s->raw());
+    } else switch (es) {
       case 1: musapy_copy_u8((const uint8_t*)a.data_ptr(), (uint8_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
       case 2: musapy_copy_u16((const uint16_t*)a.data_ptr(), (uint16_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
       case 4: musapy_copy_i32((const int32_t*)a.data_ptr(), (int32_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
       case 8: musapy_copy_i64((const int64_t*)a.data_ptr(), (int64_t*)r.data_ptr(), nd, sh.data(), st.data(), s->raw()); break;
-      default: {  // 16-byte elements: copy as pairs of 8-byte words
-        Shape sh2 = sh;
-        sh2.push_back(2);
-        Strides st2;
-        for (ssize_t x : st) st2.push_back(x * 2);
-        st2.push_back(1);
-        musapy_copy_i64((const int64_t*)a.data_ptr(), (int64_t*)r.data_ptr(), nd + 1, sh2.data(), st2.data(),
-                        s->raw());
-      }
+      default:
+        musapy_copy_c128((const musapy_c128_t*)a.data_ptr(), (musapy_c128_t*)r.data_ptr(), nd, sh.data(), st.data(),
+                         s->raw());
     }
     check_launch("contiguous");
   }

@@ -15,6 +15,8 @@
  *   oracle_unary_cplx      cpu_unary_elementwise complex arms + cpu_unary_cplx_abs
  *                                                   op_builder.rs:1904-1969
  *   oracle_cast (complex)  cpu_cast_cplx / cpu_cast_c64_c128  op_builder.rs:2080-2167
+ *   oracle_copy_bytes      cpu_copy_bytes           rust/musapy-ops/src/indexing.rs:1388-1409
+ *                          (contiguous / copy_into, indexing.rs:181-237, 816-916)
  *   oracle_cast            cpu_cast + cpu_cast_pair op_builder.rs:227-243, 2052-2097 (Rust `as`)
  *   oracle_reduce          cpu_reduce_offset/typed  op_builder.rs:3368-3394, 3496-3582
  *                          cpu_mean_typed           op_builder.rs:3585-3619
@@ -533,5 +535,15 @@ void oracle_cumsum(int dtype, int literal, const void* a, void* c, int ndim, con
     case ORACLE_F32: CUMSUM_BODY(float, float); break;
     case ORACLE_F64: CUMSUM_BODY(double, double); break;
     default: CUMSUM_BODY(int64_t, uint64_t); break;
+  }
+}
+
+/* ---- view materialisation: byte gather of each element in C order ---- */
+void oracle_copy_bytes(const void* in, void* out, int ndim, const size_t* shape, const int64_t* strides,
+                       size_t elem_size) {
+  size_t n = numel(shape, ndim);
+  for (size_t i = 0; i < n; ++i) {
+    int64_t off = oracle_offset_nd(i, shape, strides, ndim);
+    memcpy((char*)out + i * elem_size, (const char*)in + off * (int64_t)elem_size, elem_size);
   }
 }

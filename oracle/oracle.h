@@ -39,4 +39,6 @@ void oracle_reduce(int kind, int dtype, const void* a, void* c, int ndim, const 
                    const int64_t* strides, int axis, size_t axis_len, size_t out_size);
 void oracle_cumsum(int dtype, int literal, const void* a, void* c, int ndim, const size_t* shape,
                    const int64_t* strides, int axis, size_t out_size);
+void oracle_copy_bytes(const void* in, void* out, int ndim, const size_t* shape, const int64_t* strides,
+                       size_t elem_size);
 #endif

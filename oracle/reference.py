@@ -14,6 +14,7 @@ array that lives on the accelerator device (so promotion uses the GPU-narrow rul
   reduction_axis         op_builder.rs:2310-3139 (compute dtype 2209-2225, axis=None -> 1-D)
   reduce_multi / arg_reduce_multi / resolve_axes   rust/musapy-ops/src/reduction.rs:21-226
   cumsum_op              op_builder.rs:3144-3363
+  contiguous             rust/musapy-ops/src/indexing.rs:181-237 (copy_into 816-916)
 """
 from __future__ import annotations
 
@@ -338,6 +339,16 @@ def cumsum(x: np.ndarray, axis=None, literal=False) -> np.ndarray:
     if out.size:
         lib().oracle_cumsum(TCODE[ct], int(literal), _ptr(xw), _ptr(out), xw.ndim, _c(xw.shape, ctypes.c_size_t),
                             _c(_estrides(xw), ctypes.c_int64), kax, ctypes.c_size_t(out.size))
+    return out
+
+
+def contiguous(x: np.ndarray) -> np.ndarray:
+    """contiguous(): a C-ordered copy gathered element by element through the view's strides
+    (cpu_copy_bytes, indexing.rs:1388-1409); any dtype, copied as raw bytes."""
+    out = np.empty(x.shape, dtype=x.dtype)
+    if out.size:
+        lib().oracle_copy_bytes(_ptr(x), _ptr(out), x.ndim, _c(x.shape, ctypes.c_size_t),
+                                _c(_estrides(x), ctypes.c_int64), ctypes.c_size_t(x.itemsize))
     return out
 
 

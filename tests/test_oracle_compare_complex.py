@@ -213,3 +213,25 @@ def test_mixed_real_complex_binary_promotion():
     assert r.dtype == np.complex128
     r = R.binary("add", np.array([1 + 1j, 2 + 2j]), np.array([1.0, 2.0], np.float32))
     assert r.dtype == np.complex128 and r.tolist() == [2 + 1j, 4 + 2j]
+
+
+# ---- contiguous() materialisation -------------------------------------------------------------
+@pytest.mark.parametrize("dt", [np.bool_, np.int8, np.uint16, np.float16, np.int32, np.float32, np.int64,
+                                np.float64, np.complex64, np.complex128])
+def test_contiguous_matches_numpy(dt):
+    """oracle_copy_bytes (cpu_copy_bytes, indexing.rs:1388-1409) against numpy's own copy."""
+    raw = RNG.integers(0, 256, 6 * 7 * 9 * np.dtype(dt).itemsize, dtype=np.uint8)
+    x = raw.view(dt).reshape(6, 7, 9)
+    for v in (x, x.T, x.transpose(1, 0, 2), x[::-1, 2:, ::3], x[1:5:2, ::-2, 4], x[:, 3:3], x[2, 3, 4]):
+        got = R.contiguous(v)
+        want = np.array(v, order="C", copy=True)
+        assert got.shape == want.shape and got.dtype == want.dtype
+        assert got.tobytes() == want.tobytes()
+
+
+def test_contiguous_reference_known_answers():
+    """tests/python/test_indexing.py TestContiguous values."""
+    c = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], np.float32)
+    assert R.contiguous(c.T).tolist() == [[1.0, 4.0], [2.0, 5.0], [3.0, 6.0]]
+    assert R.contiguous(c[:, ::-1]).tolist() == [[3.0, 2.0, 1.0], [6.0, 5.0, 4.0]]
+    assert R.contiguous(np.arange(10, dtype=np.float32)[3:7]).tolist() == [3.0, 4.0, 5.0, 6.0]
