@@ -184,6 +184,29 @@ def all_config_ops(ms):
     return ops
 
 
+def interop_costs(ms):
+    """DLPack exchange: host time of a zero-copy export + import of a device array (no device
+    work), and the rate of importing a host (NumPy) tensor, which is a PCIe copy."""
+    a = ms.from_numpy(np.zeros((4096, 4096), np.float32))
+    v = ms.transpose(a)
+    for _ in range(100):
+        ms.from_dlpack(v)
+    n = 2000
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ms.from_dlpack(v)
+    us = (time.perf_counter() - t0) * 1e6 / n
+    h = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
+    ms.from_dlpack(h)
+    ms.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        ms.from_dlpack(h)
+    ms.synchronize()
+    gbs = 3 * h.nbytes / (time.perf_counter() - t0) / 1e9
+    return {"dlpack_roundtrip_us": round(us, 2), "host_import_GBps_pcie": round(gbs, 2)}
+
+
 def cpu_baseline(host):
     """The CPU oracle (single thread) on the same step; returns (GB/s, seconds, sample)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -288,6 +311,7 @@ def main():
                          "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4), "host_ms": round(timer.host_ms, 5)})
             print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
         line["all_configs"] = rows
+        line["interop"] = interop_costs(ms)
     print(json.dumps(line), flush=True)
 
 

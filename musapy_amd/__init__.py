@@ -23,7 +23,7 @@ except ImportError as _e:  # pragma: no cover - exercised only on an unbuilt tre
 
 from ._core import (  # noqa: F401
     Array, MusapyError, DeviceError, DeviceNotConfiguredError, DtypeError, ShapeError, MemoryError,
-    OutOfMemoryError, StreamError, KernelError,
+    OutOfMemoryError, StreamError, KernelError, InteropError,
     add, sub, mul, div, pow, sin, cos, exp, log, abs, sign, neg, clamp, astype,
     eq, ne, lt, gt, le, ge,
     sum, prod, max, min, mean, argmax, argmin, cumsum,
@@ -36,7 +36,7 @@ __all__ = [
     "Array", "Dtype", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp",
     "log", "abs", "sign", "neg", "clamp", "astype", "eq", "ne", "lt", "gt", "le", "ge", "sum", "prod", "max",
     "min", "mean", "argmax", "argmin", "cumsum", "transpose", "permute", "flip", "slice", "index_select",
-    "contiguous", "Stream", "stream", "current_stream", "synchronize",
+    "contiguous", "Stream", "stream", "current_stream", "synchronize", "from_dlpack",
 ]
 
 # dtype constants: Dtype objects that compare equal to their names and aliases
@@ -181,6 +181,74 @@ def _getitem(self: Array, key) -> Array:
     return cur
 
 
+# ---- interop: DLPack and the NumPy protocols (docs/v0.4-beta-plan-zh.md:42-43, 96-125) ----
+_KDL_CPU, _KDL_ROCM = 1, 10
+
+
+def from_dlpack(x, *, device=None, copy=None) -> Array:
+    """``ms.from_dlpack(x)``: an array from any object with ``__dlpack__`` / ``__dlpack_device__``.
+
+    A tensor on a HIP device (a PyTorch-ROCm tensor, another musapy_amd array) is adopted
+    without a copy: the producer orders its pending work before this backend's stream, and its
+    memory is handed back when the last view of the array goes.  A host tensor (NumPy, a
+    PyTorch CPU tensor) is copied to the device (``copy=False`` then raises).  ``copy=True``
+    always returns an independent array.
+    """
+    if not hasattr(x, "__dlpack__") or not hasattr(x, "__dlpack_device__"):
+        raise TypeError(f"from_dlpack: {type(x).__name__} does not implement the DLPack protocol")
+    dev_type, dev_id = x.__dlpack_device__()
+    dev_type, dev_id = int(dev_type), int(dev_id)
+    if dev_type == _KDL_ROCM:
+        if device is not None and _core._parse_device(device) != dev_id:
+            raise InteropError(f"from_dlpack: the tensor lives on hip:{dev_id}, not {device}")
+        a = _core._from_dlpack_device(x, dev_id)
+        return _core._clone(a) if copy else a
+    if dev_type == _KDL_CPU:
+        if copy is False:
+            raise BufferError("from_dlpack: a host tensor has to be copied to reach the device (copy=False)")
+        return from_numpy(_np.from_dlpack(x), device=device)
+    raise InteropError(f"from_dlpack: DLPack device type {dev_type} is neither a HIP device (10) nor the host (1)")
+
+
+def _array_protocol(self: Array, dtype=None, copy=None):
+    """``np.asarray(a)``: synchronise, copy to the host (the readback of ``numpy()``)."""
+    if copy is False:
+        raise ValueError("a device array cannot be viewed as a NumPy array without a copy")
+    host = self.numpy()
+    return host if dtype is None else host.astype(dtype, copy=False)
+
+
+# NumPy ufuncs this backend computes on the device; anything else is left to NumPy's own error
+_UFUNCS = {
+    "add": "add", "subtract": "sub", "multiply": "mul", "divide": "div", "true_divide": "div",
+    "power": "pow", "sin": "sin", "cos": "cos", "exp": "exp", "log": "log", "absolute": "abs",
+    "sign": "sign", "negative": "neg", "equal": "eq", "not_equal": "ne", "less": "lt", "greater": "gt",
+    "less_equal": "le", "greater_equal": "ge",
+}
+
+
+def _array_ufunc(self: Array, ufunc, method, *inputs, **kwargs):
+    """Strict policy: ``np.add(a, b)`` on device arrays runs the device op; mixing a device array
+    with host data raises instead of silently computing on the host."""
+    name = _UFUNCS.get(ufunc.__name__)
+    if method != "__call__" or name is None:
+        return NotImplemented
+    if any(not isinstance(v, Array) for v in inputs):
+        kinds = ", ".join(type(v).__name__ for v in inputs)
+        raise DeviceError(f"np.{ufunc.__name__}({kinds}): operands live on different devices; move host data "
+                          f"with ms.from_numpy / ms.from_dlpack, or read the device array back with .numpy()")
+    out = kwargs.pop("out", None)
+    if kwargs:
+        return NotImplemented
+    if out is not None:
+        if len(out) != 1 or not isinstance(out[0], Array):
+            return NotImplemented
+        out = out[0]
+    return globals()[name](*inputs, out=out)
+
+
+Array.__array__ = _array_protocol
+Array.__array_ufunc__ = _array_ufunc
 Array.__getitem__ = _getitem
 Array.tolist = _tolist
 Array.item = _item

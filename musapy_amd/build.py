@@ -40,7 +40,7 @@ HIP_SOURCES = [
     "kernels/scan.hip",
     "runtime/hip_runtime.cpp",
 ]
-CXX_SOURCES = ["ops/core.cpp", "ops/ops.cpp", "python/module.cpp"]
+CXX_SOURCES = ["ops/core.cpp", "ops/ops.cpp", "ops/interop.cpp", "python/module.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

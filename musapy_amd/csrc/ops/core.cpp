@@ -299,7 +299,29 @@ std::shared_ptr<Buffer> Buffer::alloc(size_t nbytes, int device, const StreamPtr
   return b;
 }
 
+std::shared_ptr<Buffer> Buffer::adopt(void* ptr, size_t nbytes, int device, const StreamPtr& stream,
+                                      std::function<void()> release) {
+  std::shared_ptr<Buffer> b(new Buffer());
+  b->ptr_ = ptr;
+  b->nbytes_ = nbytes;
+  b->device_ = device;
+  b->home_ = stream;
+  b->release_ = std::move(release);
+  return b;
+}
+
 Buffer::~Buffer() {
+  if (release_) {
+    // the owner may reuse the memory as soon as it is released: let our queued work finish
+    if (last_writer_) mpy_rt_stream_synchronize(last_writer_->raw());
+    for (auto& r : readers_) mpy_rt_stream_synchronize(r->raw());
+    if (home_) mpy_rt_stream_synchronize(home_->raw());
+    try {
+      release_();
+    } catch (...) {
+    }
+    return;
+  }
   if (!ptr_) return;
   try {
     if (last_writer_) stream_wait_stream(home_, last_writer_);

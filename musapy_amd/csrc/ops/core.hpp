@@ -12,6 +12,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -35,6 +36,7 @@ struct MemoryError : MusapyError { using MusapyError::MusapyError; };
 struct OutOfMemoryError : MemoryError { using MemoryError::MemoryError; };
 struct StreamError : MusapyError { using MusapyError::MusapyError; };
 struct KernelError : MusapyError { using MusapyError::MusapyError; };
+struct InteropError : MusapyError { using MusapyError::MusapyError; };
 
 // ---- dtypes (rust/musapy-core/src/dtype.rs:25-150) ----
 enum class Dtype : int {
@@ -118,6 +120,10 @@ void set_current_stream(StreamPtr s);
 class Buffer {
  public:
   static std::shared_ptr<Buffer> alloc(size_t nbytes, int device, const StreamPtr& stream);
+  // Device memory owned by someone else (a DLPack producer).  `release` runs when the last
+  // reference goes, after every stream that read or wrote the buffer has drained.
+  static std::shared_ptr<Buffer> adopt(void* ptr, size_t nbytes, int device, const StreamPtr& stream,
+                                       std::function<void()> release);
   ~Buffer();
   Buffer(const Buffer&) = delete;
   Buffer& operator=(const Buffer&) = delete;
@@ -129,9 +135,12 @@ class Buffer {
   void wait_reads_on(const StreamPtr& s);
   void record_read(const StreamPtr& s);
   void record_write(const StreamPtr& s);
+  const StreamPtr& home() const { return home_; }                // allocation (and free) stream
+  const StreamPtr& last_writer() const { return last_writer_; }  // null until a recorded write
 
  private:
   Buffer() = default;
+  std::function<void()> release_;   // set for adopted memory
   void* ptr_ = nullptr;
   size_t nbytes_ = 0;
   int device_ = 0;

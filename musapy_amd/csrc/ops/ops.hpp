@@ -53,6 +53,13 @@ Array reshape_merge_last(const Array& a, size_t k);
 Array reshape_split_last(const Array& a, size_t k);
 Array contiguous(const Array& a);
 
+// DLPack exchange (interop.cpp).  export_dlpack returns a DLManagedTensor* (versioned = false)
+// or a DLManagedTensorVersioned* (versioned = true) whose deleter keeps the array alive; with
+// `sync`, `consumer` waits for the array's last write.  import_dlpack adopts a producer's
+// kDLROCM tensor without a copy (ownership of `managed` passes to the returned array).
+void* export_dlpack(const Array& a, bool versioned, bool sync, hipStream_t consumer, bool copy);
+Array import_dlpack(void* managed, bool versioned);
+
 // stream resolution used by every Phase A (op_builder.rs:402-405, resolution.rs:184)
 StreamPtr pick_stream(const Array& a, const Array* out);
 

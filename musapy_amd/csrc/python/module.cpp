@@ -14,6 +14,7 @@
 #include <optional>
 
 #include "../kernels/plan.hpp"
+#include "../ops/dlpack.hpp"
 #include "../ops/ops.hpp"
 #include "../../../include/musapy_hip_runtime.h"
 #include "../../../include/musapy_kernels.h"
@@ -155,6 +156,91 @@ py::dict plan_to_dict(const mpy::Plan& p) {
 
 }  // namespace
 
+// ---- DLPack capsules (the Python side of the array API's __dlpack__ protocol) ----
+constexpr const char* kCapsule = "dltensor";
+constexpr const char* kCapsuleVersioned = "dltensor_versioned";
+
+// An unconsumed capsule still owns its tensor; a consumer renames it "used_..." when it takes it.
+void dlpack_capsule_destructor(PyObject* cap) {
+  if (PyCapsule_IsValid(cap, kCapsule)) {
+    auto* t = static_cast<DLManagedTensor*>(PyCapsule_GetPointer(cap, kCapsule));
+    if (t && t->deleter) t->deleter(t);
+  } else if (PyCapsule_IsValid(cap, kCapsuleVersioned)) {
+    auto* t = static_cast<DLManagedTensorVersioned*>(PyCapsule_GetPointer(cap, kCapsuleVersioned));
+    if (t && t->deleter) t->deleter(t);
+  }
+}
+
+py::object array_dlpack(const Array& a, py::object stream, py::object max_version, py::object dl_device,
+                        py::object copy) {
+  if (!dl_device.is_none()) {
+    auto d = dl_device.cast<std::pair<int, int>>();
+    if (d.first != kDLROCM || d.second != a.device)
+      throw py::buffer_error("__dlpack__: export to device (" + std::to_string(d.first) + ", " +
+                             std::to_string(d.second) + ") is not supported; the array lives on (10, " +
+                             std::to_string(a.device) + ")");
+  }
+  bool sync = true;
+  hipStream_t consumer = nullptr;  // None: the legacy default (null) stream
+  if (!stream.is_none()) {
+    long long v = stream.cast<long long>();
+    if (v == -1)
+      sync = false;
+    else
+      consumer = reinterpret_cast<hipStream_t>(static_cast<uintptr_t>(v));
+  }
+  bool versioned = false;
+  if (!max_version.is_none()) versioned = max_version.cast<std::pair<int, int>>().first >= 1;
+  const bool do_copy = !copy.is_none() && copy.cast<bool>();
+  void* t = export_dlpack(a, versioned, sync, consumer, do_copy);
+  PyObject* cap = PyCapsule_New(t, versioned ? kCapsuleVersioned : kCapsule, dlpack_capsule_destructor);
+  if (!cap) {
+    if (versioned) {
+      auto* v = static_cast<DLManagedTensorVersioned*>(t);
+      v->deleter(v);
+    } else {
+      auto* l = static_cast<DLManagedTensor*>(t);
+      l->deleter(l);
+    }
+    throw py::error_already_set();
+  }
+  return py::reinterpret_steal<py::object>(cap);
+}
+
+// from_dlpack for a producer on a HIP device: ask it to order its work before the stream the
+// adopted array will use, take the capsule and wrap the memory without a copy.
+Array array_from_dlpack_device(py::object obj, int device) {
+  StreamPtr s = current_stream();
+  if (!s || s->device() != device) s = default_stream(device);
+  const auto sptr = static_cast<long long>(reinterpret_cast<uintptr_t>(s->raw()));
+  py::object cap;
+  try {
+    cap = obj.attr("__dlpack__")(py::arg("stream") = sptr, py::arg("max_version") = py::make_tuple(1, 0));
+  } catch (py::error_already_set& e) {
+    if (!e.matches(PyExc_TypeError)) throw;
+    cap = obj.attr("__dlpack__")(py::arg("stream") = sptr);  // a producer without max_version
+  }
+  PyObject* c = cap.ptr();
+  bool versioned;
+  void* t;
+  if (PyCapsule_IsValid(c, kCapsuleVersioned)) {
+    versioned = true;
+    t = PyCapsule_GetPointer(c, kCapsuleVersioned);
+    auto* v = static_cast<DLManagedTensorVersioned*>(t);
+    if (v->version.major != 1)
+      throw InteropError("from_dlpack: DLPack version " + std::to_string(v->version.major) + "." +
+                         std::to_string(v->version.minor) + " is not supported");
+    if (PyCapsule_SetName(c, "used_dltensor_versioned") != 0) throw py::error_already_set();
+  } else if (PyCapsule_IsValid(c, kCapsule)) {
+    versioned = false;
+    t = PyCapsule_GetPointer(c, kCapsule);
+    if (PyCapsule_SetName(c, "used_dltensor") != 0) throw py::error_already_set();
+  } else {
+    throw InteropError("from_dlpack: __dlpack__ did not return a DLPack capsule (or it was already consumed)");
+  }
+  return import_dlpack(t, versioned);  // owns t from here on, also when it raises
+}
+
 PYBIND11_MODULE(_core, m) {
   m.doc() = "MI355X-native stride-aware elementwise / reduction backend (op layer binding)";
 
@@ -168,6 +254,7 @@ PYBIND11_MODULE(_core, m) {
   py::register_exception<OutOfMemoryError>(m, "OutOfMemoryError", mem.ptr());
   py::register_exception<StreamError>(m, "StreamError", base.ptr());
   py::register_exception<KernelError>(m, "KernelError", base.ptr());
+  py::register_exception<InteropError>(m, "InteropError", base.ptr());
 
   // streams (rust/musapy-python/src/stream.rs:14-80; lib.rs:57-70, 126-130)
   py::class_<Stream, StreamPtr>(m, "Stream")
@@ -184,6 +271,7 @@ PYBIND11_MODULE(_core, m) {
       .def_property_readonly("priority", &Stream::priority)
       .def_property_readonly("device", [](const Stream& s) { return dev_str(s.device()); })
       .def_property_readonly("id", &Stream::id)
+      .def_property_readonly("ptr", [](const Stream& s) { return reinterpret_cast<uintptr_t>(s.raw()); })
       .def_property_readonly("is_poisoned", &Stream::is_poisoned)
       .def("__eq__", [](const Stream& a, const Stream& b) { return &a == &b; })
       .def("__hash__", [](const Stream& s) { return s.id(); })
@@ -259,6 +347,10 @@ PYBIND11_MODULE(_core, m) {
       .def_property_readonly("offset", [](const Array& a) { return a.layout.offset; })
       .def_property_readonly("data_ptr", [](const Array& a) { return reinterpret_cast<uintptr_t>(a.data_ptr()); })
       .def_property_readonly("stream_ptr", [](const Array& a) { return reinterpret_cast<uintptr_t>(a.stream->raw()); })
+      // DLPack producer (array API __dlpack__ / __dlpack_device__)
+      .def("__dlpack__", &array_dlpack, py::kw_only(), py::arg("stream") = py::none(),
+           py::arg("max_version") = py::none(), py::arg("dl_device") = py::none(), py::arg("copy") = py::none())
+      .def("__dlpack_device__", [](const Array& a) { return py::make_tuple(int(kDLROCM), a.device); })
       .def("is_contiguous", [](const Array& a) { return a.is_contiguous(); })
       .def("is_0d", [](const Array& a) { return a.ndim() == 0; })
       .def("numpy", [](const Array& a) { return to_numpy(a); })
@@ -362,7 +454,19 @@ PYBIND11_MODULE(_core, m) {
 
   // host <-> device
   m.def("_from_numpy", &from_numpy, py::arg("arr"), py::arg("dtype"), py::arg("device") = py::none());
+  m.def("_from_dlpack_device", &array_from_dlpack_device, py::arg("obj"), py::arg("device"));
+  m.def("_clone", [](const Array& a) {  // an independent C-contiguous copy
+    Array c = contiguous(a);
+    if (c.data.get() != a.data.get()) return c;
+    Array r = new_array(a.shape(), a.dtype, a.device, a.stream);
+    a.data->wait_last_write_on(a.stream);
+    check_rt(mpy_rt_memcpy_d2d(r.data_ptr(), a.data_ptr(), a.nbytes(), a.stream->raw()), "copy");
+    a.data->record_read(a.stream);
+    r.data->record_write(a.stream);
+    return r;
+  });
   m.def("set_default_device", [](py::object d) { g_default_device = parse_device(d); });
+  m.def("_parse_device", [](py::object d) { return parse_device(d); });
   m.def("get_default_device", []() { return dev_str(g_default_device); });
   m.def("synchronize", [](py::object d) {
     int dv = parse_device(d);
