@@ -289,18 +289,23 @@ struct TransposeArgs {
   bool nt;                 // streaming loads
 };
 
-// Tile geometry: TL = 64 along L (output-contiguous), TP = 32 lanes x VI elements along P
-// (input-contiguous); every global access is a 16-byte vector when alignment allows.
-template <class TI> constexpr int tr_vin() { return sizeof(TI) >= 8 ? 2 : (sizeof(TI) == 4 ? 4 : 8); }
-template <class TO> constexpr int tr_vout() { return sizeof(TO) >= 8 ? 2 : (sizeof(TO) == 4 ? 4 : 8); }
-template <class TI> constexpr int tr_tp() { return 32 * tr_vin<TI>(); }
-constexpr int kTrTL = 64;
+// Tile geometry: PL lanes x VI elements along P (input-contiguous) by TL along L
+// (output-contiguous); VI / VO = elements per vector: 16 bytes, 8 for 1-byte types (which keeps
+// a u8 -> f64 tile inside LDS).  A pass of the read phase covers kBlock / PL rows of L, a pass
+// of the write phase kBlock / (TL / VO) rows of P.
+template <class T> constexpr int tr_vec() { return sizeof(T) >= 16 ? 1 : (sizeof(T) == 1 ? 8 : int(16 / sizeof(T))); }
+template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
 
-template <class F, class TO, class TI>
+template <class F, class TO, class TI, int PL, int TL>
 __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
                                                             TransposeArgs ta, F f) {
-  constexpr int VI = tr_vin<TI>(), VO = tr_vout<TO>();
-  constexpr int TP = tr_tp<TI>(), TL = kTrTL;
+  constexpr int VI = tr_vec<TI>(), VO = tr_vec<TO>();
+  constexpr int TP = tr_tp<TI, PL>();
+  constexpr int RP = kBlock / PL;  // L rows per read pass
+  static_assert(kBlock % PL == 0 && TL % RP == 0, "read passes must tile TL");
+  constexpr int NRP = TL / RP;
+  constexpr int LPW = TL / VO;     // lanes along one output row
+  static_assert(kBlock % LPW == 0 && TP % (kBlock / LPW) == 0, "write passes must tile TP");
   __shared__ TO tile[TL][TP + 1];
   const uint32_t id = blockIdx.x;
   const uint32_t bq = fd_div(ta.tilesL, id);
@@ -313,29 +318,41 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
   const TI* ab = a + off[1];
   TO* cb = c + off[0];
   const int t = threadIdx.x;
-  // read: 32 lanes x VI elements along P (unit stride in the input), 8 L-rows per pass
+  // read: PL lanes x VI elements along P (unit stride in the input), RP rows of L per pass
   {
-    const int pp = (t % 32) * VI;
+    const int pp = (t % PL) * VI;
+    const int lr = t / PL;
     const uint64_t p = p0 + pp;
-    for (int ll = t / 32; ll < TL; ll += kBlock / 32) {
-      const uint64_t l = l0 + ll;
-      if (l >= ta.L) break;
-      const TI* src = ab + int64_t(l) * ta.in_sL + int64_t(p);
-      if (ta.vec_in && p + VI <= ta.P) {
-        Vec<TI, VI> v = vload_pol<TI, VI>(src, ta.nt);
+    if (ta.vec_in && l0 + TL <= ta.L && p0 + TP <= ta.P) {
+      // interior tile: every pass's load is issued before the first LDS store
+      Vec<TI, VI> v[NRP];
 #pragma unroll
-        for (int q = 0; q < VI; ++q) tile[ll][pp + q] = f(v.v[q]);
-      } else {
+      for (int k = 0; k < NRP; ++k)
+        v[k] = vload_pol<TI, VI>(ab + int64_t(l0 + lr + k * RP) * ta.in_sL + int64_t(p), ta.nt);
 #pragma unroll
-        for (int q = 0; q < VI; ++q)
-          if (p + q < ta.P) tile[ll][pp + q] = f(src[q]);
+      for (int k = 0; k < NRP; ++k)
+#pragma unroll
+        for (int q = 0; q < VI; ++q) tile[lr + k * RP][pp + q] = f(v[k].v[q]);
+    } else {
+      for (int ll = lr; ll < TL; ll += RP) {
+        const uint64_t l = l0 + ll;
+        if (l >= ta.L) break;
+        const TI* src = ab + int64_t(l) * ta.in_sL + int64_t(p);
+        if (ta.vec_in && p + VI <= ta.P) {
+          Vec<TI, VI> v = vload_pol<TI, VI>(src, ta.nt);
+#pragma unroll
+          for (int q = 0; q < VI; ++q) tile[ll][pp + q] = f(v.v[q]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < VI; ++q)
+            if (p + q < ta.P) tile[ll][pp + q] = f(src[q]);
+        }
       }
     }
   }
   __syncthreads();
-  // write: TL/VO lanes x VO elements along L (unit stride in the output)
+  // write: LPW lanes x VO elements along L (unit stride in the output)
   {
-    constexpr int LPW = TL / VO;
     const int ll = (t % LPW) * VO;
     const uint64_t l = l0 + ll;
     for (int pp = t / LPW; pp < TP; pp += kBlock / LPW) {
@@ -354,6 +371,29 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
       }
     }
   }
+}
+
+// Launches the tiled transpose with tile (PL lanes along P) x TL; the tile is narrowed along P
+// (and lengthened along L, same LDS bytes) when P is small, so that no tile is mostly empty.
+template <class F, class TO, class TI, int PL, int TL>
+bool launch_transpose_tiles(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, hipStream_t st, F f) {
+  constexpr uint64_t TP = tr_tp<TI, PL>();
+  const uint64_t tL = (ta.L + TL - 1) / TL, tP = (ta.P + TP - 1) / TP;
+  if (tL * tP * nb >= (uint64_t(1) << 31)) return false;
+  ta.tilesL = make_fastdiv(uint32_t(tL));
+  ta.tilesP = make_fastdiv(uint32_t(tP));
+  k_unary_transpose<F, TO, TI, PL, TL><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
+  return true;
+}
+
+template <class F, class TO, class TI>
+bool launch_transpose(const TI* a, TO* c, const TransposeArgs& ta, uint64_t nb, hipStream_t st, F f) {
+  // LDS per tile: TL x (PL*VI + 1) elements of TO; 32 lanes x 64 rows is 33 KB for f32
+  if (ta.P * 4 <= uint64_t(tr_tp<TI, 32>()))
+    return launch_transpose_tiles<F, TO, TI, 8, 256>(a, c, ta, nb, st, f);
+  if (ta.P * 2 <= uint64_t(tr_tp<TI, 32>()))
+    return launch_transpose_tiles<F, TO, TI, 16, 128>(a, c, ta, nb, st, f);
+  return launch_transpose_tiles<F, TO, TI, 32, 64>(a, c, ta, nb, st, f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -513,12 +553,8 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
       ta.L = p.shape[nd - 1];
       ta.in_sL = sL;
       ta.out_sP = p.stride[0][P];
-      constexpr uint64_t TP = tr_tp<TA>(), TL = kTrTL;
-      uint64_t tL = (ta.L + TL - 1) / TL, tP = (ta.P + TP - 1) / TP;
       uint64_t nb = p.numel / (ta.P * ta.L);
-      if (tL * tP * nb < (uint64_t(1) << 31)) {
-        ta.tilesL = make_fastdiv(uint32_t(tL));
-        ta.tilesP = make_fastdiv(uint32_t(tP));
+      {
         // batch dims: all dims but P and nd-1, innermost first
         ta.batch.nd = 0;
         ta.vec_in = aligned16(a) && (uint64_t(sL < 0 ? -sL : sL) * sizeof(TA)) % 16 == 0;
@@ -533,8 +569,7 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
           if ((uint64_t(p.stride[1][d] < 0 ? -p.stride[1][d] : p.stride[1][d]) * sizeof(TA)) % 16) ta.vec_in = false;
           if ((uint64_t(p.stride[0][d]) * sizeof(TO)) % 16) ta.vec_out = false;
         }
-        k_unary_transpose<F, TO, TA><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
-        return;
+        if (launch_transpose<F, TO, TA>(a, c, ta, nb, st, f)) return;
       }
     }
   }
