@@ -25,7 +25,8 @@ constexpr int kBlock = 256;
 
 // ---------------------------------------------------------------------------------------------
 // operand access modes
-enum : int { kModeScalar = 0, kModeUnit = 1, kModeStrided = 2 };
+// kModeRev: stride -1 (a flipped row), read as vectors ending at the item and reversed in registers
+enum : int { kModeScalar = 0, kModeUnit = 1, kModeStrided = 2, kModeRev = 3 };
 
 template <class T>
 struct In {
@@ -123,6 +124,11 @@ __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t co
     Vec<T, VEC> v = vload_pol<T, VEC>(base + col, nt);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) x[k] = v.v[k];
+  } else if (mode == kModeRev && full) {
+    // elements col .. col+VEC-1 of the row sit at base-col-(VEC-1) .. base-col
+    Vec<T, VEC> v = vload_pol<T, VEC>(base - (int64_t(col) + (VEC - 1)), nt);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) x[k] = v.v[VEC - 1 - k];
   } else {
 #pragma unroll
     for (int k = 0; k < VEC; ++k)
@@ -465,7 +471,9 @@ constexpr int ew_vec() {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-inline int mode_of(int64_t s) { return s == 0 ? kModeScalar : (s == 1 ? kModeUnit : kModeStrided); }
+inline int mode_of(int64_t s) {
+  return s == 0 ? kModeScalar : (s == 1 ? kModeUnit : (s == -1 ? kModeRev : kModeStrided));
+}
 
 inline NdMeta64 make_meta64(const Plan& p) {
   NdMeta64 m{};
@@ -501,7 +509,8 @@ inline bool rows_ok(const Plan& p, int vec) {
   return true;
 }
 
-// true when every unit-stride operand starts 16-byte aligned at each VEC item of every row
+// true when every unit-stride (or reversed, stride -1) operand has each VEC item of every row
+// on one aligned vector: 16 bytes, or the item's size when that is smaller
 template <class T0, class T1, class T2 = T1>
 inline bool rows_aligned(const Plan& p, int vec, const void* c, const void* a, const void* b = nullptr) {
   uint64_t L = p.shape[p.ndim - 1];
@@ -510,8 +519,10 @@ inline bool rows_aligned(const Plan& p, int vec, const void* c, const void* a, c
   const size_t es[3] = {sizeof(T0), sizeof(T1), sizeof(T2)};
   for (int o = 0; o < p.nops; ++o) {
     int64_t s = p.stride[o][p.ndim - 1];
-    if (s != 1) continue;
-    if (es[o] * vec < 16 ? (reinterpret_cast<uintptr_t>(ptr[o]) % (es[o] * vec)) : !aligned16(ptr[o])) return false;
+    if (s != 1 && s != -1) continue;
+    // a reversed row's first item ends at the row start: its vector starts vec-1 elements lower
+    const uintptr_t q = reinterpret_cast<uintptr_t>(ptr[o]) - (s == -1 ? (vec - 1) * es[o] : 0);
+    if (es[o] * vec < 16 ? (q % (es[o] * vec)) : (q % 16)) return false;
     for (int d = 0; d < p.ndim - 1; ++d) {
       uint64_t bytes = uint64_t(p.stride[o][d] < 0 ? -p.stride[o][d] : p.stride[o][d]) * es[o];
       if (bytes % (es[o] * vec < 16 ? es[o] * vec : 16)) return false;
@@ -573,7 +584,7 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
       }
     }
   }
-  if (nd >= 2 && rows_ok(p, V)) {
+  if ((nd >= 2 || sL == -1) && rows_ok(p, V)) {
     const uint32_t L = uint32_t(p.shape[nd - 1]);
     In<TA> ia{a, mode_of(sL), nt};
     bool al = rows_aligned<TO, TA>(p, V, c, a);

@@ -139,3 +139,27 @@ def test_copy_entry_points_through_the_c_abi(name, dt):
     ms.synchronize()
     want = np.ascontiguousarray(x[::2].transpose(2, 0, 1)[::-1])
     assert_bits_equal(D.numpy(), want, f"copy {name} strided", nan_bits=True)
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.float16, np.float32, np.float64, np.complex128],
+                         ids=lambda d: np.dtype(d).name)
+def test_reversed_rows(dt):
+    """Flips of the innermost dim (stride -1) read whole vectors and reverse them in registers
+    when each row's items line up; ragged and misaligned rows take the element path."""
+    for shape in ((1 << 16,), (1000,), (7, 256), (33, 48), (5, 37), (64, 1024)):
+        x = rand(shape, dt)
+        X = ms.from_numpy(x)
+        check(ms.contiguous(ms.flip(X, len(shape) - 1)), R.contiguous(np.flip(x, -1)), f"flip {shape}")
+        if len(shape) == 2:  # offset rows: the first item no longer ends on a vector boundary
+            v = ms.slice(X, [(0, shape[0], 1), (1, shape[1], 1)])
+            check(ms.contiguous(ms.flip(v, 1)), R.contiguous(x[:, 1:][:, ::-1]), f"flip offset {shape}")
+    if dt in (np.float32, np.float64):
+        a = RNG.standard_normal((64, 1024)).astype(dt)
+        b = RNG.standard_normal((64, 1024)).astype(dt)
+        A, B = ms.from_numpy(a), ms.from_numpy(b)
+        got = ms.sub(ms.flip(A, 1), B).numpy()
+        assert_bits_equal(got, R.binary("sub", a[:, ::-1], b), "sub(flip(a), b)")
+        got = ms.exp(ms.flip(A, 1)).numpy()
+        want = R.unary("exp", a[:, ::-1])
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.all(np.abs(got - want) <= 4 * np.spacing(np.abs(want)))
