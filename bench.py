@@ -306,7 +306,7 @@ def main():
         for name, fn, bytes_ in all_config_ops(ms):
             fn(0)
             ms.synchronize()
-            t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(6)])
+            t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(20)])
             rows.append({"op": name, "ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
                          "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4), "host_ms": round(timer.host_ms, 5)})
             print(json.dumps(rows[-1]), file=sys.stderr, flush=True)

@@ -431,17 +431,14 @@ struct ColArgs {
   bool nt;            // streaming loads
 };
 
-template <class Op, class T, int VEC, int UNROLL, int WRITE>
-__global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
-                                                        bool vec_ok) {
-  using A = typename Op::A;
+// One (column group, tile) block of a column reduction: lane `lane` of wave 0 ends with the
+// block's accumulators r[v] of its VEC columns (indices relative to the tile) and first[v], the
+// elements of axis row 0 when the tile starts there.  `part` is the block's LDS for the waves.
+template <class Op, class T, int VEC, int UNROLL>
+__device__ inline void col_partial(const T* __restrict__ a, const ColArgs& ca, bool vec_ok, uint32_t t, uint32_t cg,
+                                   uint32_t outer, typename Op::A (&part)[kRBlock / kWave - 1][kWave * VEC],
+                                   typename Op::A (&acc)[VEC], T (&first)[VEC]) {
   constexpr int kWaves = kRBlock / kWave;
-  __shared__ A part[kWaves - 1][kWave * VEC];
-  const uint32_t b = blockIdx.x;
-  const uint32_t t = b % ca.tiles;
-  const uint32_t rest = b / ca.tiles;
-  const uint32_t cg = rest % ca.cgroups;
-  const uint32_t outer = rest / ca.cgroups;
   const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   int64_t off[1];
   row_offsets<1>(ca.ix, outer, off);
@@ -450,34 +447,71 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
   const bool full = vec_ok && c0 + VEC <= ca.C;
   const uint64_t k0 = uint64_t(t) * ca.chunk;
   const uint64_t k1 = k0 + ca.chunk < ca.R ? k0 + ca.chunk : ca.R;
-  A acc[VEC];
-  T first[VEC] = {};  // row 0 of the axis, kept by wave 0 for the NaN-at-0 rule
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = Op::init();
+  for (int v = 0; v < VEC; ++v) {
+    acc[v] = Op::init();
+    first[v] = T{};
+  }
   if (c0 < ca.C) {
     uint64_t k = k0 + wv;
     if (full) {
-      for (; k + (UNROLL - 1) * kWaves < k1; k += UNROLL * kWaves) {
-        Vec<T, VEC> x[UNROLL];
+      // the axis's row 0 for the NaN-at-0 rule: one extra load by wave 0 of tile 0, kept out of
+      // the streaming loop (a capture inside it cost the ordered kernels ~10% on (8192, 8192))
+      if (Op::kOrdered && k == 0 && k < k1) {
+        const Vec<T, VEC> x = vload_pol<T, VEC>(base, ca.nt);
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) x[u] = vload_pol<T, VEC>(base + int64_t(k + u * kWaves) * ca.rs, ca.nt);
-        __builtin_amdgcn_sched_barrier(0);
-        if (Op::kOrdered && k == 0)
+        for (int v = 0; v < VEC; ++v) first[v] = x.v[v];
+      }
+      // rounds of UNROLL rows (k, k + kWaves, ...).  Ordered ops are software pipelined: the
+      // next round's loads are in flight while the current one is folded -- their fold takes
+      // its first-index search in most rounds on random data, and with one wave per SIMD nothing
+      // else hides it (max over (8192, 8192) axis 0: 50.9 -> 46.2 us).  Sums keep one round in
+      // flight (pipelined: 42.9 -> 44.5 us).
+      constexpr uint64_t kStep = uint64_t(UNROLL) * kWaves;
+      const uint64_t lastu = uint64_t(UNROLL - 1) * kWaves;
+      const uint64_t rounds = k + lastu < k1 ? (k1 - k - lastu - 1) / kStep + 1 : 0;
+      Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers
+      auto load = [&](uint64_t kk, Vec<T, VEC>(&d)[UNROLL]) {
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) first[v] = x[0].v[v];
+        for (int u = 0; u < UNROLL; ++u) d[u] = vload_pol<T, VEC>(base + int64_t(kk + u * kWaves) * ca.rs, ca.nt);
+      };
+      auto fold = [&](uint64_t kk, const Vec<T, VEC>(&src)[UNROLL]) {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           T xs[UNROLL][1];
 #pragma unroll
-          for (int u = 0; u < UNROLL; ++u) xs[u][0] = x[u].v[v];
-          acc[v] = Op::template step_chunk<UNROLL, 1>(acc[v], xs, uint32_t(k - k0), uint32_t(kWaves));
+          for (int u = 0; u < UNROLL; ++u) xs[u][0] = src[u].v[v];
+          acc[v] = Op::template step_chunk<UNROLL, 1>(acc[v], xs, uint32_t(kk - k0), uint32_t(kWaves));
+        }
+      };
+      if (!Op::kOrdered) {
+        for (uint64_t i = 0; i < rounds; ++i, k += kStep) {
+          load(k, x);
+          __builtin_amdgcn_sched_barrier(0);
+          fold(k, x);
+        }
+      } else if (rounds > 0) {
+        load(k, x);
+        uint64_t i = 0;
+        for (; i + 2 < rounds; i += 2) {
+          load(k + kStep, y);
+          fold(k, x);
+          load(k + 2 * kStep, x);
+          fold(k + kStep, y);
+          k += 2 * kStep;
+        }
+        if (i + 1 < rounds) {
+          load(k + kStep, y);
+          fold(k, x);
+          fold(k + kStep, y);
+          k += 2 * kStep;
+        } else {
+          fold(k, x);
+          k += kStep;
         }
       }
       for (; k < k1; k += kWaves) {
         Vec<T, VEC> x = vload_pol<T, VEC>(base + int64_t(k) * ca.rs, ca.nt);
-        if (Op::kOrdered && k == 0)
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) first[v] = x.v[v];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[v] = Op::step(acc[v], x.v[v], int64_t(k - k0));
       }
@@ -497,16 +531,37 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
     for (int v = 0; v < VEC; ++v) part[wv - 1][lane * VEC + v] = acc[v];
   }
   __syncthreads();
-  if (wv == 0 && c0 < ca.C) {
+  if (wv == 0) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+#pragma unroll
+      for (int i = 0; i < kWaves - 1; ++i) acc[v] = Op::comb(acc[v], part[i][lane * VEC + v]);
+  }
+}
+
+template <class Op, class T, int VEC, int UNROLL, int WRITE>
+__global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
+                                                        bool vec_ok) {
+  using A = typename Op::A;
+  __shared__ A part[kRBlock / kWave - 1][kWave * VEC];
+  const uint32_t b = blockIdx.x;
+  const uint32_t t = b % ca.tiles;
+  const uint32_t rest = b / ca.tiles;
+  const uint32_t cg = rest % ca.cgroups;
+  const uint32_t outer = rest / ca.cgroups;
+  A acc[VEC];
+  T first[VEC];
+  col_partial<Op, T, VEC, UNROLL>(a, ca, vec_ok, t, cg, outer, part, acc, first);
+  const int lane = threadIdx.x % kWave;
+  const uint64_t c0 = uint64_t(cg) * kWave * VEC + uint64_t(lane) * VEC;
+  if (threadIdx.x < kWave && c0 < ca.C) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       if (c0 + v >= ca.C) break;
       A r = acc[v];
-#pragma unroll
-      for (int i = 0; i < kWaves - 1; ++i) r = Op::comb(r, part[i][lane * VEC + v]);
       if (t == 0 && ca.R > 0) r = absorb_first<Op, T>(r, first[v]);  // wave 0 walked row 0
       const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
-      write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(k0));
+      write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(t) * int64_t(ca.chunk));
     }
   }
 }
@@ -580,11 +635,14 @@ inline RowIndexer<1> out_indexer(const ReducePlan& p, int ndims) {
 inline size_t tiles_hint(const ReducePlan& p, size_t es) {
   if (p.R <= 1 || p.out_size == 0) return 1;
   if (p.kind == kColReduce) {
-    // column tiles: ~512 long-lived blocks (2 per CU) measured best; >= 64 rows per tile
+    // column tiles: ~256 long-lived blocks (one per CU, 8 loads of 16 bytes in flight per lane)
+    // measured best: (8192, 8192) f32 axis 0 at 6.3 TB/s vs 6.0 with 512 blocks of 4 loads;
+    // more concurrent row bands lose to HBM row conflicts (32 bands: 4.7-5.6 TB/s); >= 64 rows
+    // per tile
     const int vec = int(16 / es) > 0 ? int(16 / es) : 1;
     uint64_t C = p.oshape[p.ond - 1];
     uint64_t blocks = (p.out_size / C) * ceil_div(C, uint64_t(kWave) * vec);
-    const uint64_t want_blocks = 512;
+    const uint64_t want_blocks = 256;
     if (blocks >= want_blocks) return 1;
     uint64_t tiles = ceil_div(want_blocks, blocks);
     uint64_t max_tiles = ceil_div(p.R, 64);
@@ -634,7 +692,7 @@ void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, con
     for (int d = 0; d < p.ond - 1; ++d)
       if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) vec_ok = false;
     const uint64_t blocks = (p.out_size / ca.C) * ca.cgroups * ca.tiles;
-    k_reduce_col<Op, T, V, 4, WRITE><<<dim3(unsigned(blocks)), kRBlock, 0, st>>>(a, ca, out, vec_ok);
+    k_reduce_col<Op, T, V, 8, WRITE><<<dim3(unsigned(blocks)), kRBlock, 0, st>>>(a, ca, out, vec_ok);
     return;
   }
   RowArgs ra{};
@@ -716,7 +774,12 @@ bool launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t gri
 template <class Op, class OpF, class T>
 bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                          size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (out_size == 0 || out_size > kFusedMaxOutputs || axis_len == 0 || tiles < 2 || ws == nullptr) return false;
+  if (out_size == 0 || axis_len == 0 || tiles < 2 || ws == nullptr) return false;
+  // Column reductions keep two launches: folding the final into the column kernel through
+  // published slots measured slower ((8192, 8192) f32 axis 0: 48.5 us fused vs 46.3 us for
+  // partial + final at 8 tiles; 63.6 vs 47.0 at 16) -- the cross-block gather costs more than
+  // the final's launch.
+  if (out_size > kFusedMaxOutputs) return false;
   // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
   if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
   ReducePlan p;

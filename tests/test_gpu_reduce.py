@@ -276,3 +276,24 @@ def test_cumsum_deterministic():
         assert_bits_equal(ms.cumsum(Y, axis=1).numpy(), b, "row-per-block cumsum run-to-run")
     want = R.cumsum(y[:4], 1)
     assert np.all(np.abs(b[:4] - want) <= 1e-12 * np.abs(want))
+
+
+@pytest.mark.parametrize("kind", ["sum", "prod", "max", "min", "mean", "argmax", "argmin"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_column_reductions_split_into_row_tiles(kind, dt):
+    """Column reductions split into 8-64 row tiles (partial + final): ragged column groups,
+    unaligned rows, outer dims, NaN in row 0 and later rows, and argmax ties."""
+    cases = [((1024, 4096), 0), ((2048, 4096), 0), ((3, 512, 1000), 1), ((640, 2056), 0), ((4096, 260), 0)]
+    for shape, ax in cases:
+        if dt == np.int64:
+            x = RNG.integers(-50, 50, shape).astype(np.int64)
+        elif kind == "prod":
+            x = RNG.uniform(0.999, 1.001, shape).astype(dt)
+        else:
+            x = RNG.standard_normal(shape).astype(dt)
+            if kind in ("max", "min", "argmax", "argmin"):
+                x = np.round(x * 4) / 4  # plenty of ties
+                flat = np.moveaxis(x, ax, 0)
+                flat[0, ::7] = np.nan   # NaN at axis position 0 absorbs those columns
+                flat[3, 1::5] = np.nan  # later NaNs are skipped
+        check_reduce(kind, x, ax)
