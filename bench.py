@@ -113,74 +113,117 @@ def step_ops(ms):
     return ops, host
 
 
-def all_config_ops(ms):
-    """Every BASELINE config op (for the per-config table); inputs rotate over 3 copies."""
+def all_config_ops(ms, host_legs=False):
+    """Every BASELINE config op (for the per-config table); inputs rotate over 3 copies.
+
+    Rows are (name, gpu launch of launch index i, algorithmic bytes, cpu leg).  With `host_legs`
+    the BASELINE config rows carry a cpu leg: a function that runs the CPU oracle (the
+    single-threaded C restatement of musapy's CPU path) once on the same host inputs and returns
+    the algorithmic bytes it covered.  The widened rows carry none."""
     K = 3
+    R = None
+    if host_legs:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import reference as R
+
+    def leg(f, nbytes):
+        return (lambda: (f(), nbytes)[1]) if R is not None else None
+
     rng = np.random.default_rng(0)
     ops = []
     a64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
     b64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
     A64, B64 = _copies(ms, a64, K), _copies(ms, b64, K)
-    ops.append(("C1-64M add f32 67,108,864", lambda i: ms.add(A64[i % K], B64[i % K]), 12 * 67_108_864))
-    ops.append(("full sum f32 64M", lambda i: ms.sum(A64[i % K]), 4 * 67_108_864 + 4))
-    ops.append(("full argmax f32 64M", lambda i: ms.argmax(A64[i % K]), 4 * 67_108_864 + 8))
+    ops.append(("C1-64M add f32 67,108,864", lambda i: ms.add(A64[i % K], B64[i % K]), 12 * 67_108_864,
+                leg(lambda: R.binary("add", a64, b64), 12 * 67_108_864)))
+    ops.append(("full sum f32 64M", lambda i: ms.sum(A64[i % K]), 4 * 67_108_864 + 4,
+                leg(lambda: R.reduce(a64, "sum"), 4 * 67_108_864 + 4)))
+    ops.append(("full argmax f32 64M", lambda i: ms.argmax(A64[i % K]), 4 * 67_108_864 + 8,
+                leg(lambda: R.reduce(a64, "argmax"), 4 * 67_108_864 + 8)))
     r = np.random.default_rng(0)
     ca, cb = r.uniform(-1, 1, (4096, 1)).astype(np.float32), r.uniform(-1, 1, (8192,)).astype(np.float32)
     CA, CB = _copies(ms, ca, K), _copies(ms, cb, K)
-    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda i: ms.add(CA[i % K], CB[i % K]),
-                4 * 33_554_432 + 4 * 4096 + 4 * 8192))
-    xt = [ms.transpose(c) for c in _copies(ms, np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32), K)]
-    ops.append(("C2 exp transposed (8192,4096)^T", lambda i: ms.exp(xt[i % K]), 8 * 33_554_432))
+    nb = 4 * 33_554_432 + 4 * 4096 + 4 * 8192
+    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda i: ms.add(CA[i % K], CB[i % K]), nb,
+                leg(lambda: R.binary("add", ca, cb), nb)))
+    xh = np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32)
+    xt = [ms.transpose(c) for c in _copies(ms, xh, K)]
+    ops.append(("C2 exp transposed (8192,4096)^T", lambda i: ms.exp(xt[i % K]), 8 * 33_554_432,
+                leg(lambda: R.unary("exp", xh.T), 8 * 33_554_432)))
     r = np.random.default_rng(0)
-    i64 = _copies(ms, r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64), K)
-    f64 = _copies(ms, r.standard_normal((2048, 2048, 4)), K)
+    i64h = r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64)
+    f64h = r.standard_normal((2048, 2048, 4))
+    i64, f64 = _copies(ms, i64h, K), _copies(ms, f64h, K)
     N = 16_777_216
-    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda i: ms.add(i64[i % K], f64[i % K]), 24 * N))
+    sh = i64h.astype(np.float64) + f64h  # the host inputs of the later C3 steps (values only feed timing)
+    ch = np.clip(sh, -1.0, 1.0)
+    fh = ch.astype(np.float32)
+    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda i: ms.add(i64[i % K], f64[i % K]), 24 * N,
+                leg(lambda: R.binary("add", i64h, f64h), 24 * N)))
     s = [ms.add(i64[k], f64[k]) for k in range(K)]
-    ops.append(("C3 clamp f64", lambda i: ms.clamp(s[i % K], -1.0, 1.0), 16 * N))
+    ops.append(("C3 clamp f64", lambda i: ms.clamp(s[i % K], -1.0, 1.0), 16 * N,
+                leg(lambda: R.clamp(sh, -1.0, 1.0), 16 * N)))
     c = [ms.clamp(s[k], -1.0, 1.0) for k in range(K)]
-    ops.append(("C3 astype f64->f32", lambda i: ms.astype(c[i % K], "f32"), 12 * N))
+    ops.append(("C3 astype f64->f32", lambda i: ms.astype(c[i % K], "f32"), 12 * N,
+                leg(lambda: R.cast(ch, "f32"), 12 * N)))
     f = [ms.astype(c[k], "f32") for k in range(K)]
-    ops.append(("C3 astype f32->bf16", lambda i: ms.astype(f[i % K], "bf16"), 6 * N))
-    ops.append(("C3 astype f32->f16", lambda i: ms.astype(f[i % K], "f16"), 6 * N))
-    X = _copies(ms, np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32), K)
+    ops.append(("C3 astype f32->bf16", lambda i: ms.astype(f[i % K], "bf16"), 6 * N,
+                leg(lambda: R.cast(fh, "bf16"), 6 * N)))
+    ops.append(("C3 astype f32->f16", lambda i: ms.astype(f[i % K], "f16"), 6 * N,
+                leg(lambda: R.cast(fh, "f16"), 6 * N)))
+    Xh = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
+    X = _copies(ms, Xh, K)
     n = 8192 * 8192
-    ops.append(("C4 sum axis=0", lambda i: ms.sum(X[i % K], axis=0), 4 * n + 4 * 8192))
-    ops.append(("C4 mean axis=-1", lambda i: ms.mean(X[i % K], axis=-1), 4 * n + 4 * 8192))
-    ops.append(("C4 mean axis=0", lambda i: ms.mean(X[i % K], axis=0), 4 * n + 4 * 8192))
-    ops.append(("C4 max axis=(0,1)", lambda i: ms.max(X[i % K], axis=(0, 1)), 4 * n + 4))
-    ops.append(("C4 argmin axis=1", lambda i: ms.argmin(X[i % K], axis=1), 4 * n + 8 * 8192))
-    y = _copies(ms, np.random.default_rng(0).random((1024, 65536)), K)
-    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda i: ms.cumsum(y[i % K], axis=1), 16 * 1024 * 65536))
+    ops.append(("C4 sum axis=0", lambda i: ms.sum(X[i % K], axis=0), 4 * n + 4 * 8192,
+                leg(lambda: R.reduce(Xh, "sum", 0), 4 * n + 4 * 8192)))
+    ops.append(("C4 mean axis=-1", lambda i: ms.mean(X[i % K], axis=-1), 4 * n + 4 * 8192,
+                leg(lambda: R.reduce(Xh, "mean", -1), 4 * n + 4 * 8192)))
+    ops.append(("C4 mean axis=0", lambda i: ms.mean(X[i % K], axis=0), 4 * n + 4 * 8192,
+                leg(lambda: R.reduce(Xh, "mean", 0), 4 * n + 4 * 8192)))
+    ops.append(("C4 max axis=(0,1)", lambda i: ms.max(X[i % K], axis=(0, 1)), 4 * n + 4,
+                leg(lambda: R.reduce(Xh, "max", (0, 1)), 4 * n + 4)))
+    ops.append(("C4 argmin axis=1", lambda i: ms.argmin(X[i % K], axis=1), 4 * n + 8 * 8192,
+                leg(lambda: R.reduce(Xh, "argmin", 1), 4 * n + 8 * 8192)))
+    yh = np.random.default_rng(0).random((1024, 65536))
+    y = _copies(ms, yh, K)
+    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda i: ms.cumsum(y[i % K], axis=1), 16 * 1024 * 65536,
+                leg(lambda: R.cumsum(yh, axis=1), 16 * 1024 * 65536)))
+    if R is not None:
+        # musapy's literal CPU cumsum re-sums the prefix for every output (O(L^2) per row); rows
+        # are independent and cost the same, so one row's rate is the whole array's
+        ops.append(("C5 cumsum f64, literal O(L^2) CPU form (1 of 1024 rows)", None, 16 * 65536,
+                    leg(lambda: R.cumsum(yh[:1], axis=1, literal=True), 16 * 65536)))
     r = np.random.default_rng(0)
     z = (r.standard_normal((16, 1024, 1024), dtype=np.float32)
          + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
     Z = _copies(ms, z, K)
-    ops.append(("C5 c64 sum axis=(1,2)", lambda i: ms.sum(Z[i % K], axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128))
+    ops.append(("C5 c64 sum axis=(1,2)", lambda i: ms.sum(Z[i % K], axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128,
+                leg(lambda: R.reduce(z, "sum", (1, 2)), 8 * 16 * 1024 * 1024 + 128)))
     # widened rows: comparisons (1-byte bool output) and complex elementwise
     M = 16 * 1024 * 1024
-    ops.append(("cmp lt f32 64M -> bool", lambda i: ms.lt(A64[i % K], B64[i % K]), 9 * 67_108_864))
-    ops.append(("cmp eq f64 16M -> bool", lambda i: ms.eq(s[i % K], c[i % K]), 17 * N))
+    ops.append(("cmp lt f32 64M -> bool", lambda i: ms.lt(A64[i % K], B64[i % K]), 9 * 67_108_864, None))
+    ops.append(("cmp eq f64 16M -> bool", lambda i: ms.eq(s[i % K], c[i % K]), 17 * N, None))
     Z2 = [ms.neg(Z[(k + 1) % K]) for k in range(K)]
-    ops.append(("cmp eq c64 16M -> bool", lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M))
-    ops.append(("c64 mul 16M", lambda i: ms.mul(Z[i % K], Z2[i % K]), 24 * M))
-    ops.append(("c64 div 16M", lambda i: ms.div(Z[i % K], Z2[i % K]), 24 * M))
-    ops.append(("c64 abs 16M -> f32", lambda i: ms.abs(Z[i % K]), 12 * M))
-    ops.append(("astype f32->c64 64M", lambda i: ms.astype(A64[i % K], "c64"), 12 * 67_108_864))
+    ops.append(("cmp eq c64 16M -> bool", lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M, None))
+    ops.append(("c64 mul 16M", lambda i: ms.mul(Z[i % K], Z2[i % K]), 24 * M, None))
+    ops.append(("c64 div 16M", lambda i: ms.div(Z[i % K], Z2[i % K]), 24 * M, None))
+    ops.append(("c64 abs 16M -> f32", lambda i: ms.abs(Z[i % K]), 12 * M, None))
+    ops.append(("astype f32->c64 64M", lambda i: ms.astype(A64[i % K], "c64"), 12 * 67_108_864, None))
     W = [ms.astype(Z[k], "c128") for k in range(K)]
     W2 = [ms.astype(Z2[k], "c128") for k in range(K)]
-    ops.append(("c128 mul 16M", lambda i: ms.mul(W[i % K], W2[i % K]), 48 * M))
-    ops.append(("c128 div 16M", lambda i: ms.div(W[i % K], W2[i % K]), 48 * M))
+    ops.append(("c128 mul 16M", lambda i: ms.mul(W[i % K], W2[i % K]), 48 * M, None))
+    ops.append(("c128 div 16M", lambda i: ms.div(W[i % K], W2[i % K]), 48 * M, None))
     # contiguous() materialisation: 2-D transpose (transpose2d entry point), 3-D permute, flip
-    ops.append(("contiguous X^T f32 (8192,8192)", lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n))
+    ops.append(("contiguous X^T f32 (8192,8192)", lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n, None))
     P = _copies(ms, np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32), K)
     ops.append(("contiguous permute(2,0,1) f32 (8192,128,64)",
-                lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n))
-    ops.append(("contiguous flip axis=1 f32 (8192,8192)", lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n))
+                lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n, None))
+    ops.append(("contiguous flip axis=1 f32 (8192,8192)", lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n,
+                None))
     wm = (r.standard_normal((4096, 4096)) + 1j * r.standard_normal((4096, 4096))).astype(np.complex128)
     WM = _copies(ms, wm, K)
     ops.append(("contiguous ^T c128 (4096,4096)", lambda i: ms.contiguous(ms.transpose(WM[i % K])),
-                32 * 4096 * 4096))
+                32 * 4096 * 4096, None))
     return ops
 
 
@@ -303,13 +346,20 @@ def main():
                                 "sample": sample, "seconds_per_pass": round(sec, 3)}
     if args.all:
         rows = []
-        for name, fn, bytes_ in all_config_ops(ms):
-            fn(0)
-            ms.synchronize()
-            t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(20)])
-            rows.append({"op": name, "ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
-                         "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4), "host_ms": round(timer.host_ms, 5)})
-            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        for name, fn, bytes_, cpu in all_config_ops(ms, host_legs=not args.no_cpu):
+            row = {"op": name}
+            if fn is not None:
+                fn(0)
+                ms.synchronize()
+                t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(20)])
+                row.update({"ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
+                            "frac_peak": round(bytes_ / t / 1e6 / PEAK_GBS, 4), "host_ms": round(timer.host_ms, 5)})
+            if cpu is not None:  # the CPU oracle once on the same host inputs, one thread
+                t0 = time.perf_counter()
+                covered = cpu()
+                row["cpu_GBps"] = round(covered / (time.perf_counter() - t0) / 1e9, 3)
+            rows.append(row)
+            print(json.dumps(row), file=sys.stderr, flush=True)
         line["all_configs"] = rows
         line["interop"] = interop_costs(ms)
     print(json.dumps(line), flush=True)

@@ -179,6 +179,17 @@ def test_single_launch_tiled_reductions(dt):
     t[[5, 1_999_999]] = 3
     for kind in ("argmax", "argmin"):
         check_reduce(kind, t, None)
+    if dt != np.int64:
+        # blocks whose whole share is NaN publish "no element"; an all-NaN array keeps index 0
+        u = np.full(2_000_003, np.nan, dt)
+        u[1_777_777] = -5.0
+        for kind in ("max", "argmax", "min", "argmin"):
+            check_reduce(kind, u, None)
+            check_reduce(kind, np.full(2_000_003, np.nan, dt), None)
+        v = np.full(2_000_003, -np.inf, dt)
+        v[[3, 1_500_000]] = -1e30
+        for kind in ("max", "argmax", "min", "argmin"):
+            check_reduce(kind, v, None)
 
 
 @pytest.mark.parametrize("dt", [np.complex64, np.complex128])
