@@ -9,7 +9,8 @@
 //     minimum), and a freed block goes to a per-device free list tagged with the stream its free
 //     was ordered on;
 //   * an allocation on that same stream reuses the block at once -- stream order already puts the
-//     new work after every earlier use -- with no HIP call at all;
+//     new work after every earlier use -- with no HIP call at all; the most recently freed block
+//     of the class is taken first;
 //   * reuse from another stream first makes the allocating stream wait on an event recorded on
 //     the freeing stream;
 //   * a miss calls hipMalloc; when that runs out of memory, the cache is returned to the device
@@ -131,12 +132,19 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
   DevicePool& P = g_pools[device];
   auto range = P.free.equal_range(cls);
   if (range.first != range.second) {
-    auto pick = range.first;  // prefer a block freed on this stream or one with nothing pending
-    for (auto it = range.first; it != range.second; ++it)
+    // Prefer the most recently freed block of this stream (or one with nothing pending): frees
+    // are appended at the end of their size class, so walk the class backwards.  The latest
+    // block is the one most likely still held in the Infinity Cache: an op whose output is freed
+    // and allocated again each call then writes the same memory each time.  With no such block,
+    // take the oldest one, whose pending work is the most likely to be done.
+    auto pick = range.first;
+    for (auto it = range.second; it != range.first;) {
+      --it;
       if (it->second.idle || it->second.stream == stream) {
         pick = it;
         break;
       }
+    }
     Block b = pick->second;
     if (!b.idle && b.stream != stream) {
       hipError_t e = order_after(stream, b.stream);

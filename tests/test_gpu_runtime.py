@@ -75,6 +75,25 @@ def test_allocator_reuse_stats_and_empty_cache():
     assert_bits_equal(ms.mul(X, X).numpy(), x * x, "allocation after empty_cache")
 
 
+def test_allocator_hands_out_the_latest_freed_block():
+    # same stream, same size class: the most recently freed block comes back first, so an op
+    # whose result is dropped each call keeps writing the same (cache-resident) memory
+    x = RNG.standard_normal(3 << 18).astype(np.float32)
+    X = ms.from_numpy(x)
+    blocks = [ms.add(X, X) for _ in range(3)]
+    ptrs = [b.data_ptr for b in blocks]
+    del blocks[0]
+    last = blocks.pop()
+    last_ptr = last.data_ptr
+    del last
+    y = ms.add(X, X)
+    assert y.data_ptr == last_ptr and last_ptr == ptrs[2]
+    z = ms.add(X, X)
+    assert z.data_ptr == ptrs[0]
+    assert_bits_equal(y.numpy(), x + x, "reused latest block")
+    assert_bits_equal(z.numpy(), x + x, "reused earlier block")
+
+
 def test_allocator_block_reused_across_streams():
     # a block freed on s1 while s1 still reads it may be handed to s2; s2's write must wait
     x = RNG.standard_normal(1 << 24).astype(np.float32)
