@@ -1015,12 +1015,38 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
     }                                                                                                           \
     return ok ? 0 : -1;                                                                                         \
   }
+  // complex: sum, prod and mean (accumulated in f64 components, narrowed once; the mean divides by
+  // the f64 axis length, cpu_reduce_cplx, op_builder.rs:3485-3488)
+#define FUSED_CPLX(T)                                                                                           \
+  {                                                                                                             \
+    const T* x = static_cast<const T*>(a);                                                                      \
+    T* cv = static_cast<T*>(c);                                                                                 \
+    bool ok = false;                                                                                            \
+    switch (op) {                                                                                               \
+      case MUSAPY_RED_SUM:                                                                                      \
+        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,             \
+                                                        workspace_bytes, st);                                   \
+        break;                                                                                                  \
+      case MUSAPY_RED_PROD:                                                                                     \
+        ok = launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,           \
+                                                          workspace_bytes, st);                                 \
+        break;                                                                                                  \
+      case MUSAPY_RED_MEAN:                                                                                     \
+        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, double(axis_len)), RED_PASS, tiles,      \
+                                                        workspace, workspace_bytes, st);                        \
+        break;                                                                                                  \
+    }                                                                                                           \
+    return ok ? 0 : -1;                                                                                         \
+  }
   switch (dtype) {
     case MUSAPY_DT_F32: FUSED_CASE(float)
     case MUSAPY_DT_F64: FUSED_CASE(double)
     case MUSAPY_DT_I64: FUSED_CASE(int64_t)
+    case MUSAPY_DT_C64: FUSED_CPLX(musapy_c64_t)
+    case MUSAPY_DT_C128: FUSED_CPLX(musapy_c128_t)
   }
 #undef FUSED_CASE
+#undef FUSED_CPLX
   return -1;
 }
 

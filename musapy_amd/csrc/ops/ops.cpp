@@ -556,6 +556,8 @@ bool red_fused(ReduceKernel k, Dtype ct, const RedCall& c, void* out, size_t til
     case Dtype::Float32: dt = MUSAPY_DT_F32; break;
     case Dtype::Float64: dt = MUSAPY_DT_F64; break;
     case Dtype::Int64: dt = MUSAPY_DT_I64; break;
+    case Dtype::Complex64: dt = MUSAPY_DT_C64; break;
+    case Dtype::Complex128: dt = MUSAPY_DT_C128; break;
     default: return false;
   }
   return musapy_reduce_fused_v1(op, dt, c.a, out, c.nd, c.shape, c.strides, c.axis, c.axis_len, c.out_size, tiles,

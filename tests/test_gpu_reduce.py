@@ -205,6 +205,20 @@ def test_complex_reductions(dt):
         ms.max(dev(np.array([1 + 2j], np.complex128)))
 
 
+@pytest.mark.parametrize("dt", [np.complex64, np.complex128])
+def test_single_launch_complex_reductions(dt):
+    """Complex sum/mean/prod split into tiles also run as one launch (four workspace words per
+    slot); back-to-back calls check that the workspace is left clean."""
+    z = (RNG.standard_normal((5, 400_000)) + 1j * RNG.standard_normal((5, 400_000))).astype(dt)
+    Z = dev(z)
+    for kind in ("sum", "mean", "sum"):
+        check_reduce(kind, z, 1, gpu_x=Z)
+        check_reduce(kind, z, None, gpu_x=Z)
+    zp = np.exp(1j * RNG.uniform(-1e-3, 1e-3, (3, 300_000))).astype(dt)
+    check_reduce("prod", zp, 1)
+    check_reduce("prod", np.ascontiguousarray(zp[0]), None)
+
+
 def test_reduce_errors_and_edges():
     x = dev(np.ones((2, 3), np.float32))
     with pytest.raises(ms.ShapeError):
