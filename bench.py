@@ -140,6 +140,13 @@ def all_config_ops(ms, host_legs=False):
                 leg(lambda: R.reduce(a64, "sum"), 4 * 67_108_864 + 4)))
     ops.append(("full argmax f32 64M", lambda i: ms.argmax(A64[i % K]), 4 * 67_108_864 + 8,
                 leg(lambda: R.reduce(a64, "argmax"), 4 * 67_108_864 + 8)))
+    # the same whole-array reductions at 4x the size: the fixed end-of-launch hand-over amortised
+    a256 = np.random.default_rng(1).uniform(-1, 1, 268_435_456).astype(np.float32)
+    A256 = _copies(ms, a256, K)
+    ops.append(("full sum f32 256M", lambda i: ms.sum(A256[i % K]), 4 * 268_435_456 + 4,
+                leg(lambda: R.reduce(a256, "sum"), 4 * 268_435_456 + 4)))
+    ops.append(("full argmax f32 256M", lambda i: ms.argmax(A256[i % K]), 4 * 268_435_456 + 8,
+                leg(lambda: R.reduce(a256, "argmax"), 4 * 268_435_456 + 8)))
     r = np.random.default_rng(0)
     ca, cb = r.uniform(-1, 1, (4096, 1)).astype(np.float32), r.uniform(-1, 1, (8192,)).astype(np.float32)
     CA, CB = _copies(ms, ca, K), _copies(ms, cb, K)

@@ -74,6 +74,30 @@ def test_binary_broadcast(sa, sb):
     assert_bits_equal(got, R.binary("div", b, a), f"broadcast {sb}/{sa}")
 
 
+def test_long_broadcast_rows():
+    """Long output rows (>= 512 f32 / 256 f64 elements) take the row-piece kernel: ragged row
+    lengths, a partial last piece group, the length threshold, f64, reversed and strided operands,
+    and comparison / complex outputs through the same launcher."""
+    cases = [((300, 1), (1001,), np.float32), ((257, 1), (5000,), np.float32), ((64, 1), (512,), np.float32),
+             ((9, 1), (511,), np.float32), ((130, 1), (2049,), np.float64), ((3, 40, 1), (40, 777), np.float32)]
+    for sa, sb, dt in cases:
+        a = RNG.uniform(-1, 1, sa).astype(dt)
+        b = RNG.uniform(-1, 1, sb).astype(dt)
+        assert_bits_equal(ms.sub(dev(a), dev(b)).numpy(), R.binary("sub", a, b), f"rows {sa}-{sb} {np.dtype(dt).name}")
+        assert_bits_equal(ms.lt(dev(a), dev(b)).numpy(), R.compare("lt", a, b), f"lt rows {sa},{sb}")
+    base = RNG.uniform(-1, 1, (200, 3000)).astype(np.float32)
+    row = RNG.uniform(-1, 1, (3000,)).astype(np.float32)
+    B, Rw = dev(base), dev(row)
+    assert_bits_equal(ms.mul(ms.flip(B, 1), Rw).numpy(), R.binary("mul", np.ascontiguousarray(base[:, ::-1]), row),
+                      "reversed rows x broadcast row")
+    got = ms.add(ms.slice(B, [(0, 200, 1), (0, 3000, 2)]), ms.slice(Rw, [(1, 3000, 2)])).numpy()
+    assert_bits_equal(got, R.binary("add", np.ascontiguousarray(base[:, ::2]), np.ascontiguousarray(row[1::2])),
+                      "stride-2 rows + stride-2 row")
+    z = (RNG.standard_normal((64, 1)) + 1j * RNG.standard_normal((64, 1))).astype(np.complex64)
+    w = (RNG.standard_normal(3000) + 1j * RNG.standard_normal(3000)).astype(np.complex64)
+    assert_bits_equal(ms.mul(dev(z), dev(w)).numpy(), R.binary("mul", z, w), "c64 broadcast rows", nan_bits=True)
+
+
 def test_binary_sizes_and_tails():
     for n in (1, 3, 255, 256, 1023, 1024, 1025, 4097, 65537, 1 << 20):
         a = RNG.standard_normal(n).astype(np.float32)
