@@ -280,8 +280,9 @@ def cpu_baseline(host):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards with no "
-              f"exchange (see DESIGN.md) and this build runs on single-GPU boxes.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build runs on single-GPU "
+              f"boxes. Elementwise ops and axis reductions shard over the non-reduced dims with no exchange; a "
+              f"whole-array reduction adds one exchange of a scalar per GPU.", file=sys.stderr)
         sys.exit(2)
     import musapy_amd as ms
 

@@ -69,7 +69,8 @@ def test_c4_sum_mean(c4, kind, axis):
         scale /= 8192
     err = np.abs(got.astype(np.float64) - want)
     assert np.all(err <= 1e-5 * scale), err.max()
-    # report the elementwise figure too (finding 4 of the survey: it is not a usable bound)
+    # also against the exact (f64) sum: a relative bound per element against the sequential CPU
+    # sum is not usable, since that sum is itself up to n*eps*sum|x| away from the exact one
     exact = np.sum(x.astype(np.float64), axis=axis) / (8192 if kind == "mean" else 1)
     assert np.max(np.abs(got - exact) / scale) < 1e-6
 
