@@ -151,3 +151,31 @@ def test_reductions_random_views(chunk):
         scale = np.sum(np.abs(x.astype(np.float64)), axis=ax, keepdims=keep)
         assert got.shape == want.shape, what
         assert np.all(np.abs(got.astype(np.float64) - want) <= TOL[dt] * scale + 1e-30), f"sum {what}"
+
+
+def rand_mixed(rng, shape, dt):
+    if np.dtype(dt).kind == "i":
+        return rng.integers(-1000, 1001, shape).astype(dt)
+    return rand_data(rng, shape, dt)
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_mixed_dtype_random_layouts(chunk):
+    """Operands of different dtypes (promotion fused into the op, or cast first) in random views."""
+    rng = np.random.default_rng(4000 + chunk)
+    pairs = [(np.int64, np.float64), (np.int64, np.float32), (np.int32, np.float64), (np.float32, np.float64),
+             (np.int32, np.float32), (np.float32, np.complex64), (np.float64, np.complex64)]
+    for case in range(100):
+        ta, tb = pairs[case % len(pairs)]
+        if rng.random() < 0.5:
+            ta, tb = tb, ta
+        shape_a = rand_shape(rng, int(rng.integers(1, 4)))
+        base = rand_mixed(rng, shape_a, ta)
+        a, A = random_view(rng, base, ms.from_numpy(base), max_ops=2)
+        a = np.ascontiguousarray(a)
+        shape_b = broadcast_partner(rng, a.shape)
+        b = rand_mixed(rng, shape_b, tb)
+        B = ms.from_numpy(b)
+        op = ("add", "sub", "mul")[case % 3]
+        what = f"chunk {chunk} case {case}: {np.dtype(ta).name}{a.shape} {op} {np.dtype(tb).name}{b.shape}"
+        assert_bits_equal(getattr(ms, op)(A, B).numpy(), R.binary(op, a, b), what)
