@@ -69,6 +69,14 @@ void note_alloc(size_t n) {
   g_count.fetch_add(1);
 }
 
+// The return value of a runtime call.  A failing HIP call also leaves its code as the thread's
+// "last error", which the next launch check would report against an unrelated kernel; the
+// caller is told here instead, so the sticky copy is consumed.
+int rc(hipError_t e) {
+  if (e != hipSuccess) (void)hipGetLastError();
+  return int(e);
+}
+
 // make `waiter` wait for everything queued so far on `target`
 hipError_t order_after(hipStream_t waiter, hipStream_t target) {
   hipEvent_t ev = nullptr;
@@ -104,15 +112,15 @@ __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
 
 extern "C" {
 
-int mpy_rt_device_count(int* count) { return int(hipGetDeviceCount(count)); }
+int mpy_rt_device_count(int* count) { return rc(hipGetDeviceCount(count)); }
 
-int mpy_rt_set_device(int device) { return int(hipSetDevice(device)); }
+int mpy_rt_set_device(int device) { return rc(hipSetDevice(device)); }
 
 int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_mem, int* cu_count, int* arch_major,
                        int* arch_minor) {
   hipDeviceProp_t prop;
   hipError_t e = hipGetDeviceProperties(&prop, device);
-  if (e != hipSuccess) return int(e);
+  if (e != hipSuccess) return rc(e);
   if (name && name_len) {
     std::strncpy(name, prop.gcnArchName, name_len - 1);
     name[name_len - 1] = 0;
@@ -126,7 +134,7 @@ int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_me
 
 int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
   *ptr = nullptr;
-  if (device < 0 || device >= kMaxDevices) return int(hipErrorInvalidDevice);
+  if (device < 0 || device >= kMaxDevices) return rc(hipErrorInvalidDevice);
   const size_t cls = size_class(nbytes ? nbytes : 1);  // a valid, unique pointer even for empty arrays
   std::lock_guard<std::mutex> lk(g_mu);
   DevicePool& P = g_pools[device];
@@ -148,7 +156,7 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
     Block b = pick->second;
     if (!b.idle && b.stream != stream) {
       hipError_t e = order_after(stream, b.stream);
-      if (e != hipSuccess) return int(e);
+      if (e != hipSuccess) return rc(e);
     }
     P.free.erase(pick);
     P.cached_bytes -= b.size;
@@ -161,7 +169,7 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
     return 0;
   }
   hipError_t e = hipSetDevice(device);
-  if (e != hipSuccess) return int(e);
+  if (e != hipSuccess) return rc(e);
   void* p = nullptr;
   e = hipMalloc(&p, cls);
   if (e == hipErrorOutOfMemory) {
@@ -173,7 +181,7 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
   }
   if (e != hipSuccess) {
     (void)hipGetLastError();  // leave no sticky error for the next launch check
-    return int(e);
+    return rc(e);
   }
   P.live[p] = Block{p, cls, nbytes, stream, false};
   note_alloc(nbytes);
@@ -197,7 +205,7 @@ int mpy_rt_free(void* ptr, hipStream_t stream) {
     P.cached_bytes += b.size;
     return 0;
   }
-  return int(hipFree(ptr));  // not from this allocator
+  return rc(hipFree(ptr));  // not from this allocator
 }
 
 int mpy_rt_empty_cache(int device) {
@@ -208,30 +216,30 @@ int mpy_rt_empty_cache(int device) {
     hipError_t e = release_cached_locked(d);
     if (first == hipSuccess) first = e;
   }
-  return int(first);
+  return rc(first);
 }
 
 int mpy_rt_memcpy_h2d(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
   hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return int(e);
-  return int(hipStreamSynchronize(s));  // the host buffer may be released right after
+  if (e != hipSuccess) return rc(e);
+  return rc(hipStreamSynchronize(s));  // the host buffer may be released right after
 }
 int mpy_rt_memcpy_d2h(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
   hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s);
-  if (e != hipSuccess) return int(e);
-  return int(hipStreamSynchronize(s));
+  if (e != hipSuccess) return rc(e);
+  return rc(hipStreamSynchronize(s));
 }
 int mpy_rt_memcpy_d2d(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
-  return int(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s));
+  return rc(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s));
 }
 
 int mpy_rt_stream_create(hipStream_t* stream, int device) {
   hipError_t e = hipSetDevice(device);
-  if (e != hipSuccess) return int(e);
-  return int(hipStreamCreateWithFlags(stream, hipStreamNonBlocking));
+  if (e != hipSuccess) return rc(e);
+  return rc(hipStreamCreateWithFlags(stream, hipStreamNonBlocking));
 }
 int mpy_rt_stream_destroy(hipStream_t stream) {
   // cached blocks last freed on this stream outlive it: drain it, then mark them idle so no
@@ -247,23 +255,23 @@ int mpy_rt_stream_destroy(hipStream_t stream) {
     }
   }
   hipError_t e2 = hipStreamDestroy(stream);
-  return int(e != hipSuccess ? e : e2);
+  return rc(e != hipSuccess ? e : e2);
 }
-int mpy_rt_stream_synchronize(hipStream_t stream) { return int(hipStreamSynchronize(stream)); }
-int mpy_rt_device_synchronize(void) { return int(hipDeviceSynchronize()); }
+int mpy_rt_stream_synchronize(hipStream_t stream) { return rc(hipStreamSynchronize(stream)); }
+int mpy_rt_device_synchronize(void) { return rc(hipDeviceSynchronize()); }
 
 int mpy_rt_event_create(hipEvent_t* ev, int timing) {
-  return int(hipEventCreateWithFlags(ev, timing ? hipEventDefault : hipEventDisableTiming));
+  return rc(hipEventCreateWithFlags(ev, timing ? hipEventDefault : hipEventDisableTiming));
 }
-int mpy_rt_event_destroy(hipEvent_t ev) { return int(hipEventDestroy(ev)); }
-int mpy_rt_event_record(hipEvent_t ev, hipStream_t s) { return int(hipEventRecord(ev, s)); }
-int mpy_rt_stream_wait_event(hipStream_t s, hipEvent_t ev) { return int(hipStreamWaitEvent(s, ev, 0)); }
-int mpy_rt_event_synchronize(hipEvent_t ev) { return int(hipEventSynchronize(ev)); }
-int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t a, hipEvent_t b) { return int(hipEventElapsedTime(ms, a, b)); }
+int mpy_rt_event_destroy(hipEvent_t ev) { return rc(hipEventDestroy(ev)); }
+int mpy_rt_event_record(hipEvent_t ev, hipStream_t s) { return rc(hipEventRecord(ev, s)); }
+int mpy_rt_stream_wait_event(hipStream_t s, hipEvent_t ev) { return rc(hipStreamWaitEvent(s, ev, 0)); }
+int mpy_rt_event_synchronize(hipEvent_t ev) { return rc(hipEventSynchronize(ev)); }
+int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t a, hipEvent_t b) { return rc(hipEventElapsedTime(ms, a, b)); }
 
 int mpy_rt_check_launch(void) {
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return int(e);
+  if (e != hipSuccess) return rc(e);
   const int w = musapy_kernels_take_error();
   return w ? -w : 0;
 }
