@@ -12,7 +12,9 @@
  * stream is immediate and host-only, reuse from another stream is ordered by an event, and a
  * miss calls hipMalloc (after returning the cache to the device when memory runs out).  No call
  * blocks the host on device work except the copies to/from host memory and the synchronizes.
- * All functions return 0 on success or a hipError_t code (negative: a kernel-wrapper error).
+ * All functions return 0 on success or a hipError_t code (negative: a kernel-wrapper error).  A
+ * failing call also clears HIP's per-thread "last error", so that code is reported once, by the
+ * call that caused it, and not again by the next mpy_rt_check_launch.
  * Streams are always created with the default priority.
  */
 #ifndef MUSAPY_HIP_RUNTIME_H
