@@ -327,7 +327,9 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
 /* ---- wrapper-level error (new; no counterpart in kernels.rs) ----
  * Returns and clears the calling thread's last wrapper error: 0 none, 1 a cumsum scratch buffer
  * that is NULL or smaller than the reference's scratch formula requires, 2 a reduction whose
- * per-tile length reaches 2^31 elements (pass more tiles). */
+ * per-tile length reaches 2^31 elements (pass more tiles), 3 ndim outside [0, 32] or an axis
+ * outside [0, ndim) (32 is the reference's MUSAPY_MAX_NDIM).  A wrapper that reports an error
+ * launches nothing. */
 int musapy_kernels_take_error(void);
 
 /* ---- planning helper (new; no counterpart in kernels.rs) ----

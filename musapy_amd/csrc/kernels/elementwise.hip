@@ -525,7 +525,7 @@ template <class F, class TO, class TA>
 void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize_t* as, hipStream_t st, F f) {
   Plan p;
   const ssize_t* ins[1] = {as};
-  if (!plan_elementwise(p, ndim, shape, 1, ins)) return;
+  if (!args_ok(ndim) || !plan_elementwise(p, ndim, shape, 1, ins)) return;
   // the narrower type moves 16 bytes per item, the wider one 16-32 (e.g. f64->f32: 4 elements)
   constexpr int V = ew_vec<TA, TO>();
   const bool nt = operand_elems(p, 1) * sizeof(TA) >= kStreamLoadBytes;
@@ -593,7 +593,7 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
                    hipStream_t st, F f) {
   Plan p;
   const ssize_t* ins[2] = {as, bs};
-  if (!plan_elementwise(p, ndim, shape, 2, ins)) return;
+  if (!args_ok(ndim) || !plan_elementwise(p, ndim, shape, 2, ins)) return;
   constexpr int V = vec_of<T>();
   const int nd = p.ndim;
   const bool nt = (operand_elems(p, 1) + operand_elems(p, 2)) * sizeof(T) >= kStreamLoadBytes;
@@ -647,7 +647,7 @@ void launch_binary_mixed(const void* a, const void* b, void* c, int ndim, const 
                          const ssize_t* bs, hipStream_t st, F f) {
   Plan p;
   const ssize_t* ins[2] = {as, bs};
-  if (!plan_elementwise(p, ndim, shape, 2, ins)) return;
+  if (!args_ok(ndim) || !plan_elementwise(p, ndim, shape, 2, ins)) return;
   const TA* pa = static_cast<const TA*>(a);
   const TB* pb = static_cast<const TB*>(b);
   TC* pc = static_cast<TC*>(c);

@@ -143,8 +143,18 @@ __device__ inline T shfl_xor(T v, int m) {
 }
 
 // Wrapper-level error of the calling thread (read and cleared by musapy_kernels_take_error):
-// 1 = cumsum scratch missing or too small, 2 = a reduction tile longer than 2^31 elements.
+// 1 = cumsum scratch missing or too small, 2 = a reduction tile longer than 2^31 elements,
+// 3 = ndim outside [0, 32] or axis outside [0, ndim).
 inline thread_local int g_wrapper_error = 0;
+
+// The ranks and axes the planners accept: 0 <= ndim <= kMaxDims (the reference's
+// MUSAPY_MAX_NDIM, elementwise.mu:16) and, for a reduction or scan of a non-scalar, 0 <= axis <
+// ndim.  A wrapper called outside them launches nothing and reports error 3.
+inline bool args_ok(int ndim, int axis = 0) {
+  if (ndim >= 0 && ndim <= kMaxDims && (ndim == 0 || (axis >= 0 && axis < ndim))) return true;
+  g_wrapper_error = 3;
+  return false;
+}
 
 // interleaved complex elements, the ABI types themselves
 using c64 = musapy_c64_t;

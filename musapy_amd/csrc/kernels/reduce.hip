@@ -665,6 +665,7 @@ template <class Op, class T, int WRITE>
 void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                    size_t axis_len, size_t out_size, size_t tiles, hipStream_t st) {
   if (out_size == 0) return;  // axis_len == 0 still writes the identity (0 for sums, 1 for products)
+  if (!args_ok(ndim, axis)) return;
   if (tiles < 1) tiles = 1;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
@@ -782,6 +783,7 @@ bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shap
   if (out_size > kFusedMaxOutputs) return false;
   // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
   if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
+  if (!args_ok(ndim, axis)) return false;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
   if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return false;
@@ -864,6 +866,7 @@ extern "C" {
 size_t musapy_reduce_tiles_hint(int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis,
                                 size_t axis_len, size_t out_size, size_t elem_size) {
   if (out_size == 0 || axis_len == 0) return 1;
+  if (ndim < 0 || ndim > kMaxDims || (ndim > 0 && (axis < 0 || axis >= ndim))) return 1;  // the launch reports it
   ReducePlan p;
   plan_reduce(p, ndim, in_shape, in_strides, axis, axis_len, out_size);
   return tiles_hint(p, elem_size);

@@ -320,6 +320,7 @@ template <class T>
 void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                    size_t axis_len, size_t out_size, hipStream_t st) {
   if (out_size == 0 || axis_len == 0) return;
+  if (!args_ok(ndim, axis)) return;
   ScanPlan p;
   plan_scan(p, ndim, shape, strides, axis);
   constexpr uint64_t TILE = uint64_t(kSBlock) * scan_items<T>();

@@ -365,6 +365,10 @@ Array Array::view(const Layout& l) const {
 }
 
 Array new_array(const Shape& shape, Dtype dtype, int device, const StreamPtr& stream) {
+  // the kernels' rank limit (the reference's MUSAPY_MAX_NDIM, elementwise.mu:16); views and
+  // broadcasts never exceed the rank of an array that was created
+  if (shape.size() > 32)
+    throw ShapeError("arrays have at most 32 dimensions (got " + std::to_string(shape.size()) + ")");
   Array a;
   a.layout = Layout::from_shape(shape);
   a.dtype = dtype;

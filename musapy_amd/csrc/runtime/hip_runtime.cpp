@@ -179,10 +179,7 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
     hipSetDevice(device);
     e = hipMalloc(&p, cls);
   }
-  if (e != hipSuccess) {
-    (void)hipGetLastError();  // leave no sticky error for the next launch check
-    return rc(e);
-  }
+  if (e != hipSuccess) return rc(e);
   P.live[p] = Block{p, cls, nbytes, stream, false};
   note_alloc(nbytes);
   *ptr = p;
@@ -279,6 +276,7 @@ int mpy_rt_check_launch(void) {
 const char* mpy_rt_error_string(int code) {
   if (code == -1) return "kernel wrapper error: cumsum scratch buffer missing or too small";
   if (code == -2) return "kernel wrapper error: a reduction tile reaches 2^31 elements (pass more tiles)";
+  if (code == -3) return "kernel wrapper error: ndim outside [0, 32] or axis outside [0, ndim)";
   if (code < 0) return "kernel wrapper error";
   return hipGetErrorString(hipError_t(code));
 }
