@@ -434,11 +434,11 @@ struct ColArgs {
 // One (column group, tile) block of a column reduction: lane `lane` of wave 0 ends with the
 // block's accumulators r[v] of its VEC columns (indices relative to the tile) and first[v], the
 // elements of axis row 0 when the tile starts there.  `part` is the block's LDS for the waves.
-template <class Op, class T, int VEC, int UNROLL>
+template <class Op, class T, int VEC, int UNROLL, int BS = kRBlock>
 __device__ inline void col_partial(const T* __restrict__ a, const ColArgs& ca, bool vec_ok, uint32_t t, uint32_t cg,
-                                   uint32_t outer, typename Op::A (&part)[kRBlock / kWave - 1][kWave * VEC],
+                                   uint32_t outer, typename Op::A (&part)[BS / kWave - 1][kWave * VEC],
                                    typename Op::A (&acc)[VEC], T (&first)[VEC]) {
-  constexpr int kWaves = kRBlock / kWave;
+  constexpr int kWaves = BS / kWave;
   const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   int64_t off[1];
   row_offsets<1>(ca.ix, outer, off);
@@ -539,11 +539,10 @@ __device__ inline void col_partial(const T* __restrict__ a, const ColArgs& ca, b
   }
 }
 
-template <class Op, class T, int VEC, int UNROLL, int WRITE>
-__global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
-                                                        bool vec_ok) {
+template <class Op, class T, int VEC, int UNROLL, int WRITE, int BS = kRBlock>
+__global__ __launch_bounds__(BS) void k_reduce_col(const T* __restrict__ a, ColArgs ca, RedOut<T> out, bool vec_ok) {
   using A = typename Op::A;
-  __shared__ A part[kRBlock / kWave - 1][kWave * VEC];
+  __shared__ A part[BS / kWave - 1][kWave * VEC];
   const uint32_t b = blockIdx.x;
   const uint32_t t = b % ca.tiles;
   const uint32_t rest = b / ca.tiles;
@@ -551,7 +550,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_col(const T* __restrict__ a,
   const uint32_t outer = rest / ca.cgroups;
   A acc[VEC];
   T first[VEC];
-  col_partial<Op, T, VEC, UNROLL>(a, ca, vec_ok, t, cg, outer, part, acc, first);
+  col_partial<Op, T, VEC, UNROLL, BS>(a, ca, vec_ok, t, cg, outer, part, acc, first);
   const int lane = threadIdx.x % kWave;
   const uint64_t c0 = uint64_t(cg) * kWave * VEC + uint64_t(lane) * VEC;
   if (threadIdx.x < kWave && c0 < ca.C) {
@@ -693,7 +692,13 @@ void launch_reduce(const T* a, RedOut<T> out, int ndim, const size_t* shape, con
     for (int d = 0; d < p.ond - 1; ++d)
       if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) vec_ok = false;
     const uint64_t blocks = (p.out_size / ca.C) * ca.cgroups * ca.tiles;
-    k_reduce_col<Op, T, V, 8, WRITE><<<dim3(unsigned(blocks)), kRBlock, 0, st>>>(a, ca, out, vec_ok);
+    // sums: 8 waves with 4 rows of loads each (42.4-42.7 us for the (8192, 8192) f32 axis-0
+    // partial, against 43.4-43.9 with 4 waves x 8 rows); ordered ops keep 4 waves x 8 rows
+    // (46.0 us, against 46.9-47.3 with 8 waves): their pipelined fold wants the registers
+    if constexpr (Op::kOrdered)
+      k_reduce_col<Op, T, V, 8, WRITE, 256><<<dim3(unsigned(blocks)), 256, 0, st>>>(a, ca, out, vec_ok);
+    else
+      k_reduce_col<Op, T, V, 4, WRITE, 512><<<dim3(unsigned(blocks)), 512, 0, st>>>(a, ca, out, vec_ok);
     return;
   }
   RowArgs ra{};
