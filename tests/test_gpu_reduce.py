@@ -100,6 +100,34 @@ def test_ordered_semantics_planted(kind):
     check_reduce(kind, z.T.copy(), 0)
 
 
+@pytest.mark.parametrize("kind", ["max", "min"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_two_axis_max_min_semantics(kind, dt):
+    """max/min over (0, 1) of a 2-D array run as the axis-0 partial plus one fused final (or, when
+    the axis-0 pass is not split, as two passes); either way the result is the reference's
+    axis-0-then-axis-1 one: a NaN heading column 0 absorbs everything, a NaN heading another
+    column drops that column from the second pass, later NaNs are skipped, +-0 ties keep the first."""
+    for shape in ((3000, 64), (64, 3000), (4096, 1000), (70000, 3)):
+        if dt == np.int64:
+            check_reduce(kind, RNG.integers(-5, 6, shape).astype(np.int64), (0, 1))
+            continue
+        x = RNG.integers(-2, 3, shape).astype(dt)
+        x[0, 1] = np.nan          # drops column 1 from the second pass
+        x[7, ::3] = np.nan        # later NaNs are skipped
+        x[:, 2] = -0.0
+        check_reduce(kind, x, (0, 1))
+        y = x.copy()
+        y[0, 0] = np.nan          # absorbs everything
+        check_reduce(kind, y, (0, 1))
+        z = np.full(shape, np.nan, dt)
+        z[0, 1], z[5, 1], z[9, 2] = 1.0, 3.0, 7.0  # column 2's head is NaN: its 7.0 is dropped
+        check_reduce(kind, z, (0, 1))
+        w = np.zeros(shape, dt)
+        w[:, ::2] = -0.0          # the first column's zero decides the bits
+        check_reduce(kind, w, (0, 1))
+        check_reduce(kind, np.ascontiguousarray(w[:, ::-1]), (0, 1))
+
+
 @pytest.mark.parametrize("kind", ["sum", "max", "argmax", "mean"])
 def test_reduce_views(kind):
     base = RNG.standard_normal((64, 96)).astype(np.float32)
