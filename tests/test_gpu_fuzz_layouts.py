@@ -179,3 +179,28 @@ def test_mixed_dtype_random_layouts(chunk):
         op = ("add", "sub", "mul")[case % 3]
         what = f"chunk {chunk} case {case}: {np.dtype(ta).name}{a.shape} {op} {np.dtype(tb).name}{b.shape}"
         assert_bits_equal(getattr(ms, op)(A, B).numpy(), R.binary(op, a, b), what)
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_cumsum_random_views(chunk):
+    """cumsum over a random axis (or flattened) of random views: f32/f64 to the sum bound, i64 exact."""
+    rng = np.random.default_rng(5000 + chunk)
+    for case in range(60):
+        dt = (np.float32, np.float64, np.int64)[case % 3]
+        shape = tuple(d if d else 2 for d in rand_shape(rng, int(rng.integers(1, 4))))
+        base = rand_mixed(rng, shape, dt)
+        x, X = random_view(rng, base, ms.from_numpy(base))
+        x = np.ascontiguousarray(x)
+        axis = None if rng.random() < 0.2 else int(rng.integers(-x.ndim, x.ndim))
+        what = f"chunk {chunk} case {case}: {np.dtype(dt).name} {x.shape} axis={axis}"
+        got = ms.cumsum(X, axis=axis).numpy()
+        want = R.cumsum(x, axis=axis)
+        assert got.shape == want.shape and got.dtype == want.dtype, what
+        if dt == np.int64:
+            assert np.array_equal(got, want), what
+            continue
+        # each prefix is a sum: bound it by tol * (running sum of |x|) along the same axis
+        ax = 0 if axis is None else axis
+        xa = np.abs(x.reshape(-1) if axis is None else x).astype(np.float64)
+        scale = np.cumsum(xa, axis=ax)
+        assert np.all(np.abs(got.astype(np.float64) - want) <= TOL[dt] * scale + 1e-30), what
