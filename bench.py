@@ -257,6 +257,20 @@ def interop_costs(ms):
     return {"dlpack_roundtrip_us": round(us, 2), "host_import_GBps_pcie": round(gbs, 2)}
 
 
+def host_cpu():
+    """The host the CPU baseline ran on: CPU model and logical CPU count (one thread is used)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "threads_used": 1}
+
+
 def cpu_baseline(host):
     """The CPU oracle (single thread) on the same step; returns (GB/s, seconds, sample)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -351,7 +365,7 @@ def main():
     if not args.no_cpu:
         v, sec, sample = cpu_baseline(host)
         line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                                "sample": sample, "seconds_per_pass": round(sec, 3)}
+                                "sample": sample, "seconds_per_pass": round(sec, 3), "host": host_cpu()}
     if args.all:
         rows = []
         for name, fn, bytes_, cpu in all_config_ops(ms, host_legs=not args.no_cpu):
