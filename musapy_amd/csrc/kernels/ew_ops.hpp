@@ -173,29 +173,19 @@ struct ToBf16F {
   }
 };
 
-// f32 -> IEEE binary16 bits, round to nearest even, computed on the bit pattern so the result
-// does not depend on the FP mode registers.
+// f32 -> IEEE binary16 bits, round to nearest even.  Numbers go through v_cvt_f16_f32 (kernels
+// run in the default FP mode: round to nearest even, binary16 subnormals kept), which measured
+// 15.3 us for C3's 16M elements against 16.6 us for an integer restatement on the bit pattern;
+// NaNs are built on the bit pattern.
 struct ToF16F {
   __device__ uint16_t operator()(float v) const {
-    uint32_t u = __float_as_uint(v);
-    uint32_t sign = (u >> 16) & 0x8000u;
-    uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return uint16_t(sign | 0x7e00u | ((a >> 13) & 0x3ffu));  // NaN
-    if (a >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // >= 65520 rounds to inf
-    if (a >= 0x38800000u) {  // normal binary16 range (>= 2^-14)
-      uint32_t r = a - 0x38000000u;  // rebias exponent 127 -> 15
-      r = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
-      return uint16_t(sign | r);
-    }
-    if (a <= 0x33000000u) return uint16_t(sign);  // <= 2^-25: ties-to-even gives 0
-    uint32_t e = a >> 23;                      // 103..112
-    uint32_t m = (a & 0x7fffffu) | 0x800000u;  // value = m * 2^(e-150)
-    uint32_t sh = 126u - e;                    // quantum 2^-24  ->  q = m >> (126 - e)
-    uint32_t q = m >> sh;
-    uint32_t rem = m & ((1u << sh) - 1u);
-    uint32_t half = 1u << (sh - 1u);
-    if (rem > half || (rem == half && (q & 1u))) ++q;
-    return uint16_t(sign | q);
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t a = u & 0x7fffffffu;
+    // NaN: quiet, sign and the top 10 payload bits kept (the hardware conversion does not keep them)
+    if (a > 0x7f800000u) return uint16_t(((u >> 16) & 0x8000u) | 0x7e00u | ((a >> 13) & 0x3ffu));
+    // everything else: v_cvt_f16_f32, IEEE round-to-nearest-even with binary16 subnormals kept and
+    // overflow to infinity -- the same bits as the integer RNE restatement of the oracle
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
   }
 };
 
