@@ -167,9 +167,10 @@ template <> struct CastF<musapy_c64_t, musapy_c128_t> {
 // f32 -> bfloat16 bits, round to nearest even.  NaN keeps sign and leading payload, quiet bit set.
 struct ToBf16F {
   __device__ uint16_t operator()(float v) const {
-    uint32_t u = __float_as_uint(v);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x0040u);
-    return uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    const uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x0040u);  // NaN: quiet, payload kept
+    // v_cvt_pk_bf16_f32: round to nearest even, the same bits as (u + 0x7fff + lsb) >> 16
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
   }
 };
 
