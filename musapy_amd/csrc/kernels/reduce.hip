@@ -73,11 +73,46 @@ __device__ inline typename Op::A absorb_first(typename Op::A acc, T first) {
 }
 
 // --------------------------------------------------------------------------------------------
+// A whole wave's f32 max/min accumulators with tile-relative int32 indices, combined by one
+// unsigned 64-bit max per butterfly step instead of Op::comb on (value, index).  The key's high
+// word orders the values (sign-magnitude bits mapped to unsigned order, inverted for min), its
+// low word is ~index, so among equal values the lowest index wins, and an empty accumulator
+// (key 0) loses to every element.  +0 and -0 compare equal and so share a key (the +0 bits); when
+// a zero wins, its sign is read back from the lane that holds the winning index.  Lane values are
+// never NaN here (the scan skips NaNs; the NaN-at-position-0 rule is applied after the combine),
+// so the result is bit-identical to folding Op::comb over the wave.
+template <class Op>
+__device__ inline VI<float, int32_t> wave_reduce_ext_f32(VI<float, int32_t> a) {
+  constexpr bool kMax = Op::kMax;
+  uint32_t u = __builtin_bit_cast(uint32_t, a.val);
+  if ((u & 0x7fffffffu) == 0) u = 0;  // -0 -> +0
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (!kMax) u = ~u;
+  uint64_t key = a.idx < 0 ? 0 : (uint64_t(u) << 32) | uint32_t(~uint32_t(a.idx));
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) {
+    const uint64_t o = acc_shfl(key, m);
+    key = o > key ? o : key;
+  }
+  if (key == 0) return VI<float, int32_t>{0.0f, -1};
+  const int32_t idx = int32_t(~uint32_t(key));
+  uint32_t v = uint32_t(key >> 32);
+  if (!kMax) v = ~v;
+  v = (v & 0x80000000u) ? (v & 0x7fffffffu) : ~v;
+  if (v == 0) {  // a zero won (the same key on every lane): take its sign from its lane
+    const bool neg = a.idx == idx && (__builtin_bit_cast(uint32_t, a.val) >> 31);
+    if (__ballot(neg) != 0) v = 0x80000000u;
+  }
+  return VI<float, int32_t>{__builtin_bit_cast(float, v), idx};
+}
+
 // Group reduction (GROUP lanes -> lane 0 of the group holds the result).
 template <class Op, int GROUP>
 __device__ inline typename Op::A group_reduce(typename Op::A acc) {
   using A = typename Op::A;
-  if constexpr (GROUP > 1) {
+  if constexpr (GROUP >= kWave && Op::kOrdered && std::is_same_v<A, VI<float, int32_t>>) {
+    acc = wave_reduce_ext_f32<Op>(acc);
+  } else if constexpr (GROUP > 1) {
     constexpr int W = GROUP < kWave ? GROUP : kWave;
 #pragma unroll
     for (int m = W / 2; m >= 1; m >>= 1) acc = Op::comb(acc, acc_shfl(acc, m));

@@ -130,6 +130,7 @@ struct OpExt {
   using Idx = I;
   static constexpr bool kOrdered = true;
   static constexpr bool kArg = ARG;
+  static constexpr bool kMax = MAX;
   __device__ static bool better(T a, T b) { return MAX ? (a > b) : (a < b); }
   __device__ static A init() { return A{T(0), -1}; }
   // elements of one lane arrive in increasing k, so a tie never replaces the kept element
@@ -164,15 +165,20 @@ struct OpExt {
     const bool improve = acc.idx < 0 ? !is_nan(m) : better(m, acc.val);
     if (improve) {
       uint32_t off = 0;
-      T val = m;
 #pragma unroll
       for (int u = U - 1; u >= 0; --u)
 #pragma unroll
         for (int v = V - 1; v >= 0; --v)
-          if (x[u][v] == m) {
-            off = u * stepk + v;
-            val = x[u][v];
-          }
+          if (x[u][v] == m) off = u * stepk + v;
+      // equal to m means the same bits, except that -0 equals +0: keep the first zero's bits
+      T val = m;
+      if (m == T(0)) {
+#pragma unroll
+        for (int u = U - 1; u >= 0; --u)
+#pragma unroll
+          for (int v = V - 1; v >= 0; --v)
+            if (x[u][v] == m) val = x[u][v];
+      }
       acc = A{val, I(base + int64_t(k + off))};
     }
     return acc;

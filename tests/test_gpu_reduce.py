@@ -100,6 +100,39 @@ def test_ordered_semantics_planted(kind):
     check_reduce(kind, z.T.copy(), 0)
 
 
+@pytest.mark.parametrize("kind", ["max", "min", "argmax", "argmin"])
+@pytest.mark.parametrize("n", [300, 8192, 20000])
+def test_f32_row_combine_edge_values(kind, n):
+    """Unit-stride f32 rows, whose lanes combine (value, index) through one packed 64-bit key per
+    step: infinities, all-NaN rows, subnormals, +-0 ties in both orders and ties spread over lanes
+    and waves, each row also negated (min sees the mirror case)."""
+    rows = np.empty((12, n), np.float32)
+    rows[0] = -np.inf                                        # every element -inf
+    rows[1] = np.nan
+    rows[1, n - 1] = -np.inf                                 # one element, the last
+    rows[2] = -1.0
+    rows[2, 100], rows[2, n // 2] = -0.0, 0.0                # -0 first, then +0
+    rows[3] = -1.0
+    rows[3, 100], rows[3, n // 2] = 0.0, -0.0                # +0 first, then -0
+    rows[4] = np.where(RNG.random(n) < 0.5, -0.0, 0.0)
+    rows[4, 7] = -0.0
+    rows[5] = RNG.uniform(-1, 1, n)
+    rows[5, [n - 5, 200, n // 3]] = 3.0                      # ties in different lanes and waves
+    rows[6] = -0.0
+    rows[6, 50] = np.float32(1e-45)                          # the smallest subnormal
+    rows[6, n - 50] = np.float32(-1e-45)
+    rows[7] = RNG.uniform(-1, 1, n)
+    rows[7, [n - 1, n - 100]] = np.inf
+    rows[8] = RNG.uniform(-1, 1, n)
+    rows[8, 0] = np.nan                                      # NaN at position 0 absorbs
+    rows[9] = np.nan                                         # all NaN
+    rows[10] = RNG.standard_normal(n)
+    rows[10, ::3] = np.nan
+    rows[11] = np.float32(2.5)                               # one value everywhere: index 0
+    check_reduce(kind, rows, 1)
+    check_reduce(kind, -rows, 1)
+
+
 @pytest.mark.parametrize("kind", ["max", "min"])
 @pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
 def test_two_axis_max_min_semantics(kind, dt):
