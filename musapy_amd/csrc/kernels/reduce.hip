@@ -73,16 +73,18 @@ __device__ inline typename Op::A absorb_first(typename Op::A acc, T first) {
 }
 
 // --------------------------------------------------------------------------------------------
-// A whole wave's f32 max/min accumulators with tile-relative int32 indices, combined by one
+// A whole wave's f32 max/min accumulators whose indices are below 2^32 - 1 (tile-relative int32,
+// or absolute int64 in a whole-array reduction of fewer elements), combined by one
 // unsigned 64-bit max per butterfly step instead of Op::comb on (value, index).  The key's high
 // word orders the values (sign-magnitude bits mapped to unsigned order, inverted for min), its
 // low word is ~index, so among equal values the lowest index wins, and an empty accumulator
 // (key 0) loses to every element.  +0 and -0 compare equal and so share a key (the +0 bits); when
 // a zero wins, its sign is read back from the lane that holds the winning index.  Lane values are
-// never NaN here (the scan skips NaNs; the NaN-at-position-0 rule is applied after the combine),
-// so the result is bit-identical to folding Op::comb over the wave.
-template <class Op>
-__device__ inline VI<float, int32_t> wave_reduce_ext_f32(VI<float, int32_t> a) {
+// never NaN here (the scan skips NaNs; the NaN-at-position-0 rule is applied after the combine,
+// and a combiner that folds an absorbed NaN overrides its result with it afterwards), so the
+// result is bit-identical to folding Op::comb over the wave.
+template <class Op, class I>
+__device__ inline VI<float, I> wave_reduce_ext_f32(VI<float, I> a) {
   constexpr bool kMax = Op::kMax;
   uint32_t u = __builtin_bit_cast(uint32_t, a.val);
   if ((u & 0x7fffffffu) == 0) u = 0;  // -0 -> +0
@@ -94,8 +96,8 @@ __device__ inline VI<float, int32_t> wave_reduce_ext_f32(VI<float, int32_t> a) {
     const uint64_t o = acc_shfl(key, m);
     key = o > key ? o : key;
   }
-  if (key == 0) return VI<float, int32_t>{0.0f, -1};
-  const int32_t idx = int32_t(~uint32_t(key));
+  if (key == 0) return VI<float, I>{0.0f, I(-1)};
+  const I idx = I(~uint32_t(key));
   uint32_t v = uint32_t(key >> 32);
   if (!kMax) v = ~v;
   v = (v & 0x80000000u) ? (v & 0x7fffffffu) : ~v;
@@ -103,15 +105,25 @@ __device__ inline VI<float, int32_t> wave_reduce_ext_f32(VI<float, int32_t> a) {
     const bool neg = a.idx == idx && (__builtin_bit_cast(uint32_t, a.val) >> 31);
     if (__ballot(neg) != 0) v = 0x80000000u;
   }
-  return VI<float, int32_t>{__builtin_bit_cast(float, v), idx};
+  return VI<float, I>{__builtin_bit_cast(float, v), idx};
 }
 
-// Group reduction (GROUP lanes -> lane 0 of the group holds the result).
+// Group reduction (GROUP lanes -> lane 0 of the group holds the result).  `idx32`: the caller's
+// int64 indices are all below 2^32 - 1 and no lane holds a NaN it must keep, so f32 max/min
+// accumulators may take the packed-key wave combine (int32 indices always do).
 template <class Op, int GROUP>
-__device__ inline typename Op::A group_reduce(typename Op::A acc) {
+__device__ inline typename Op::A group_reduce(typename Op::A acc, bool idx32 = false) {
   using A = typename Op::A;
-  if constexpr (GROUP >= kWave && Op::kOrdered && std::is_same_v<A, VI<float, int32_t>>) {
+  constexpr bool kKeyed = GROUP >= kWave && Op::kOrdered;
+  if constexpr (kKeyed && std::is_same_v<A, VI<float, int32_t>>) {
     acc = wave_reduce_ext_f32<Op>(acc);
+  } else if constexpr (kKeyed && std::is_same_v<A, VI<float, int64_t>>) {
+    if (idx32) {
+      acc = wave_reduce_ext_f32<Op>(acc);
+    } else {
+#pragma unroll
+      for (int m = kWave / 2; m >= 1; m >>= 1) acc = Op::comb(acc, acc_shfl(acc, m));
+    }
   } else if constexpr (GROUP > 1) {
     constexpr int W = GROUP < kWave ? GROUP : kWave;
 #pragma unroll
@@ -416,7 +428,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
                                                             true, f, acc, int64_t(c * kChunk));
       if (c == 0) first = f;
     }
-    acc = group_reduce<OpF, kRowBS>(acc);
+    acc = group_reduce<OpF, kRowBS>(acc, n < 0xffffffffull);
     if (threadIdx.x == 0) {
       if (b == 0 && n > 0) acc = absorb_first<OpF, T>(acc, first);
       uint32_t s[W];
@@ -444,7 +456,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
 #pragma unroll
     for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
   }
-  r = group_reduce<OpF, kRowBS>(r);
+  r = group_reduce<OpF, kRowBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
   if (threadIdx.x == 0) {
     if constexpr (Op::kOrdered) {
       if (first.idx == 0 && is_nan(first.val)) r = first;  // block 0 absorbed a NaN at position 0
