@@ -65,7 +65,8 @@ int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop);
 
 /* After a kernel-ABI call: returns the pending launch error (hipGetLastError) or, if none, the
  * kernel library's own wrapper error negated (musapy_kernels_take_error: -1 cumsum scratch,
- * -2 reduction tile too long). */
+ * -2 reduction tile too long, -3 bad rank or axis, -4 cumsum extent past 32 bits, -5 no-alloc
+ * scratch too small). */
 int mpy_rt_check_launch(void);
 const char* mpy_rt_error_string(int code);
 

@@ -328,9 +328,28 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
  * Returns and clears the calling thread's last wrapper error: 0 none, 1 a cumsum scratch buffer
  * that is NULL or smaller than the reference's scratch formula requires, 2 a reduction whose
  * per-tile length reaches 2^31 elements (pass more tiles), 3 ndim outside [0, 32] or an axis
- * outside [0, ndim) (32 is the reference's MUSAPY_MAX_NDIM).  A wrapper that reports an error
+ * outside [0, ndim) (32 is the reference's MUSAPY_MAX_NDIM), 4 a cumsum with 2^32 or more rows
+ * (or a dimension outside the scanned axis of 2^32 or more).  A wrapper that reports an error
  * launches nothing. */
 int musapy_kernels_take_error(void);
+
+/* ---- device wait faults (new; no counterpart in kernels.rs) ----
+ * Two kernels wait for another workgroup's result: the combiner of musapy_reduce_fused_v1 and
+ * the look-back of a cumsum whose rows are split into tiles.  Each wait polls a bounded number
+ * of times; when that runs out, the kernel records a fault in a per-device word, does not write
+ * a result it cannot trust (the reduction skips its output; the scan carries on with a zero
+ * prefix), and exits normally.  Results of the work queued since the last check are then
+ * invalid, as after a failed kernel (the reference surfaces such errors at stream
+ * synchronisation, rust/musapy-core/src/stream.rs:311-377).
+ * musapy_kernels_take_fault(device): call after synchronizing the streams whose work it should
+ * cover; returns 0 (no fault), a bit set of 1 (a reduction combiner gave up) and 2 (a scan
+ * look-back gave up) and clears the word, or -1 when the device cannot be queried.  After a fault,
+ * a workspace given to musapy_reduce_fused_v1 may hold stale slots: zero it before reuse.
+ * musapy_kernels_set_spin_limit(polls): sets how many polls a wait makes before it gives up
+ * (default 2^24) and returns the previous value; 0 makes every wait give up at once, which lets
+ * tests drive the error path while every kernel still exits normally. */
+int musapy_kernels_take_fault(int device);
+uint32_t musapy_kernels_set_spin_limit(uint32_t polls);
 
 /* ---- planning helper (new; no counterpart in kernels.rs) ----
  * Tiles per output that the partial entry points should be given for this reduction on this

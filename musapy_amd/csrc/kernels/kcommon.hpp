@@ -144,8 +144,23 @@ __device__ inline T shfl_xor(T v, int m) {
 
 // Wrapper-level error of the calling thread (read and cleared by musapy_kernels_take_error):
 // 1 = cumsum scratch missing or too small, 2 = a reduction tile longer than 2^31 elements,
-// 3 = ndim outside [0, 32] or axis outside [0, ndim).
+// 3 = ndim outside [0, 32] or axis outside [0, ndim), 4 = a scan with 2^32 or more rows (or a
+// non-axis extent of 2^32 or more), 5 = a no-alloc reduction that needs more than the static
+// scratch holds.
 inline thread_local int g_wrapper_error = 0;
+
+// ---------------------------------------------------------------------------------------------
+// Bounded device waits.  The kernels that wait for another workgroup's result (the combiner of a
+// single-launch reduction, the look-back of a row scan) poll at most `wait_spin_limit()` times.
+// When that runs out they stop waiting, OR their fault code into the device's fault word, skip
+// or finish their work, and exit normally -- so a grid always drains.  The host reads and clears
+// the word after a synchronize (musapy_kernels_take_fault).
+enum : uint32_t { kFaultReduceWait = 1u, kFaultScanWait = 2u };
+// polls a bounded wait may make (default 2^24; musapy_kernels_set_spin_limit)
+uint32_t wait_spin_limit();
+// device address of the current device's fault word, nullptr when it cannot be resolved (the
+// first call on a device zeroes it with a kernel on `st`)
+uint32_t* device_fault_word(hipStream_t st);
 
 // The ranks and axes the planners accept: 0 <= ndim <= kMaxDims (the reference's
 // MUSAPY_MAX_NDIM, elementwise.mu:16) and, for a reduction or scan of a non-scalar, 0 <= axis <

@@ -17,6 +17,9 @@
 #include "publish.hpp"
 #include "../../../include/musapy_kernels.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace mpy {
 
 constexpr int kRBlock = 256;
@@ -259,13 +262,15 @@ constexpr size_t kFusedMaxOutputs = 64;
 constexpr size_t kFusedMaxTiles = 2048;  // <= 8 * kRowBS (the largest PER dispatched)
 struct FusedArgs {
   uint64_t* slots;
-  uint32_t spin_limit;
+  uint32_t* fault;      // the device's fault word (kcommon.hpp)
+  uint32_t spin_limit;  // polls the combiner may make before it gives up
 };
 
 // Gathers the published W-word slots lane, lane + kRowBS, ... (below `count`) into v: all
 // outstanding slots' words are loaded together, the ready ones kept, the rest polled again.
+// Returns false when the poll budget ran out with slots still unpublished.
 template <int W, int PER>
-__device__ inline void gather_published(const uint64_t* slots, uint32_t count, uint32_t spin_limit,
+__device__ inline bool gather_published(const uint64_t* slots, uint32_t count, uint32_t spin_limit,
                                         uint64_t (&v)[PER][W]) {
   uint32_t pending = 0;
 #pragma unroll
@@ -289,6 +294,16 @@ __device__ inline void gather_published(const uint64_t* slots, uint32_t count, u
     }
     if (pending) __builtin_amdgcn_s_sleep(2);
   }
+  return pending == 0;
+}
+
+// After a combiner's gather: true when any lane of the block gave up.  Thread 0 then records the
+// fault; the block skips its output write (the caller raises an error instead of returning a
+// wrong value).
+__device__ inline bool combiner_gave_up(bool ok, uint32_t* fault) {
+  const bool bad = __syncthreads_or(ok ? 0 : 1) != 0;
+  if (bad && threadIdx.x == 0 && fault) atomicOr(fault, kFaultReduceWait);
+  return bad;
 }
 
 // a tile's accumulator (tile-relative int32 index) as the final's accumulator (absolute index)
@@ -333,7 +348,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
   const uint64_t o = w - ra.nwork;
   uint64_t* row_slots = fa.slots + o * ra.tiles * W;
   uint64_t v[PER][W];
-  gather_published<W, PER>(row_slots, ra.tiles, fa.spin_limit, v);
+  const bool ok = gather_published<W, PER>(row_slots, ra.tiles, fa.spin_limit, v);
   AF r = OpF::init();
   A first{};
 #pragma unroll
@@ -350,6 +365,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
 #pragma unroll
     for (int i = 0; i < W; ++i) st_relaxed(row_slots + uint64_t(tt) * W + i, 0);
   }
+  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
   r = group_reduce<OpF, kRowBS>(r);
   if (threadIdx.x == 0) {
     if constexpr (Op::kOrdered) {
@@ -439,7 +455,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
   }
   // combiner: lane l folds block results l, l + 512, ... (PER of them at most)
   uint64_t v[PER][W];
-  gather_published<W, PER>(fa.slots, grid, fa.spin_limit, v);
+  const bool ok = gather_published<W, PER>(fa.slots, grid, fa.spin_limit, v);
   AF r = OpF::init();
   AF first{};
 #pragma unroll
@@ -456,6 +472,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
 #pragma unroll
     for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
   }
+  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
   r = group_reduce<OpF, kRowBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
   if (threadIdx.x == 0) {
     if constexpr (Op::kOrdered) {
@@ -818,38 +835,51 @@ template <class T> inline RedOut<T> vout(T* c) { return RedOut<T>{c, nullptr, 0.
 template <class T> inline RedOut<T> iout(int64_t* c) { return RedOut<T>{nullptr, c, 0.0, kFinPlain}; }
 template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c, nullptr, cnt, kFinMean}; }
 
-template <class Op, class OpF, class T>
-bool launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
-                             hipStream_t st);
+// what a single-launch launcher did
+enum : int { kFusedLaunched = 0, kFusedNotCovered = -1, kFusedNoRoom = -2 };
 
-// the fused single launch for a row-kind reduction split into `tiles` tiles; false (nothing
-// launched) when the shape does not take the 512-lane block path or the workspace is too small
 template <class Op, class OpF, class T>
-bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
-                         size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (out_size == 0 || axis_len == 0 || tiles < 2 || ws == nullptr) return false;
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
+                            hipStream_t st);
+
+// The fused single launch for a row-kind reduction split into `tiles` tiles.  kFusedNotCovered
+// (nothing launched) when the shape does not take the 512-lane block path, kFusedNoRoom when the
+// workspace is too small for its slots.
+template <class Op, class OpF, class T>
+int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                        size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (out_size == 0 || axis_len == 0 || tiles < 2 || ws == nullptr) return kFusedNotCovered;
   // Column reductions keep two launches: folding the final into the column kernel through
   // published slots measured slower ((8192, 8192) f32 axis 0: 48.5 us fused vs 46.3 us for
   // partial + final at 8 tiles; 63.6 vs 47.0 at 16) -- the cross-block gather costs more than
   // the final's launch.
-  if (out_size > kFusedMaxOutputs) return false;
+  if (out_size > kFusedMaxOutputs) return kFusedNotCovered;
   // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
   if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
-  if (!args_ok(ndim, axis)) return false;
+  if (!args_ok(ndim, axis)) return kFusedNotCovered;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
-  if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return false;
+  if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return kFusedNotCovered;
   for (int d = 0; d < p.ond; ++d)
-    if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return false;
+    if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return kFusedNotCovered;
   // one output over one contiguous run: the persistent grid (1024 blocks measured best for 64M
   // f32: sum 6.5, argmax 6.1 TB/s against 6.1 / 5.9 with one block per tile)
-  if (out_size == 1 && launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, 1024, ws, ws_bytes, st)) return true;
+  if (out_size == 1) {
+    const int r = launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, 1024, ws, ws_bytes, st);
+    if (r != kFusedNotCovered) return r;
+  }
   constexpr int V = rvec<T>();
   uint64_t chunk = ceil_div(ceil_div(p.R, tiles), uint64_t(V)) * V;
-  if (chunk * sizeof(T) < 16384 || chunk >= (uint64_t(1) << 31)) return false;
+  if (chunk * sizeof(T) < 16384 || chunk >= (uint64_t(1) << 31)) return kFusedNotCovered;
+  if (uint64_t(out_size) * tiles >= (uint64_t(1) << 31)) return kFusedNotCovered;
   const uint64_t W = sizeof(typename Op::A) / 4;
   const uint64_t words = uint64_t(out_size) * tiles * W;
-  if (words * 8 > ws_bytes || uint64_t(out_size) * tiles >= (uint64_t(1) << 31)) return false;
+  if (words * 8 > ws_bytes) return kFusedNoRoom;
+  FusedArgs fa{};
+  fa.slots = static_cast<uint64_t*>(ws);
+  fa.fault = device_fault_word(st);
+  fa.spin_limit = wait_spin_limit();
+  if (fa.fault == nullptr) return kFusedNotCovered;  // a wait that expired could not be reported
   RowArgs ra{};
   ra.nt = true;
   ra.ix = out_indexer(p, p.ond);
@@ -858,9 +888,6 @@ bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shap
   ra.tiles = uint32_t(tiles);
   ra.chunk = chunk;
   ra.nwork = uint64_t(out_size) * tiles;
-  FusedArgs fa{};
-  fa.slots = static_cast<uint64_t*>(ws);
-  fa.spin_limit = 1u << 24;
   // streaming blocks first, then one combiner per output
   const dim3 grid(unsigned(ra.nwork + out_size));
   switch (ceil_div(tiles, uint64_t(kRowBS))) {
@@ -868,30 +895,32 @@ bool launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shap
     case 2: k_reduce_row_fused<Op, OpF, T, V, 4, 2><<<grid, kRowBS, 0, st>>>(a, ra, out, fa); break;
     default: k_reduce_row_fused<Op, OpF, T, V, 4, 4><<<grid, kRowBS, 0, st>>>(a, ra, out, fa); break;
   }
-  return true;
+  return kFusedLaunched;
 }
 
 // whole-array reduction of `n` contiguous, 16-byte aligned elements on a persistent grid of
-// `grid` blocks plus a combiner; false when not applicable (nothing launched)
+// `grid` blocks plus a combiner
 template <class Op, class OpF, class T>
-bool launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
-                             hipStream_t st) {
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
+                            hipStream_t st) {
   constexpr int V = rvec<T>();
   constexpr uint64_t kChunk = uint64_t(kRowBS) * 4 * V;
-  if (n == 0 || ws == nullptr || !al16(a)) return false;
+  if (n == 0 || ws == nullptr || !al16(a)) return kFusedNotCovered;
   const uint64_t nchunks = ceil_div(n, kChunk);
   if (grid > nchunks) grid = uint32_t(nchunks);
-  if (grid < 2 || grid > 2 * kRowBS) return false;
+  if (grid < 2 || grid > 2 * kRowBS) return kFusedNotCovered;
   const uint64_t W = sizeof(typename OpF::A) / 4;
-  if (uint64_t(grid) * W * 8 > ws_bytes) return false;
+  if (uint64_t(grid) * W * 8 > ws_bytes) return kFusedNoRoom;
   FusedArgs fa{};
   fa.slots = static_cast<uint64_t*>(ws);
-  fa.spin_limit = 1u << 24;
+  fa.fault = device_fault_word(st);
+  fa.spin_limit = wait_spin_limit();
+  if (fa.fault == nullptr) return kFusedNotCovered;
   if (grid <= kRowBS)
     k_reduce_all_fused<Op, OpF, T, V, 4, 1><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
   else
     k_reduce_all_fused<Op, OpF, T, V, 4, 2><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
-  return true;
+  return kFusedLaunched;
 }
 
 }  // namespace mpy
@@ -908,6 +937,111 @@ template <class T> using OpArgmax = OpExt<T, true, true>;
 template <class T> using OpArgmin = OpExt<T, false, true>;
 template <class T> using OpArgmax64 = OpExt<T, true, true, int64_t>;  // over (value, absolute index) partials
 template <class T> using OpArgmin64 = OpExt<T, false, true, int64_t>;
+
+// --------------------------------------------------------------------------------------------
+// Device-resident state of the library: the fault word of the bounded waits.  Each GPU the
+// library runs on holds its own copy until the process ends.  In host code the variable's name is
+// a host-side stand-in, not a device address: the kernels are only ever given the address that
+// hipGetSymbolAddress returns for the current device (DeviceState).
+static __device__ __align__(256) uint32_t wait_fault;
+
+constexpr int kMaxDevices = 64;
+struct DeviceState {
+  uint32_t* fault;    // device address of `wait_fault` on this device
+};
+std::mutex g_state_mu;
+std::atomic<bool> g_state_ready[kMaxDevices];
+DeviceState g_state[kMaxDevices];
+std::atomic<uint32_t> g_spin_limit{1u << 24};
+
+__global__ void k_zero_words(uint64_t* w, uint64_t n) {
+  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x)
+    w[i] = 0;
+}
+
+// The current device's state, resolved once per device with that device current.  The first call
+// on a device also zeroes the fault word with a kernel on `st` (ordered before the caller's work
+// on that stream).  nullptr when a HIP call fails.
+const DeviceState* device_state(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (g_state_ready[dev].load(std::memory_order_acquire)) return &g_state[dev];
+  std::lock_guard<std::mutex> lk(g_state_mu);
+  if (!g_state_ready[dev].load(std::memory_order_relaxed)) {
+    void* f = nullptr;
+    if (hipGetSymbolAddress(&f, HIP_SYMBOL(wait_fault)) != hipSuccess || f == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_state[dev].fault = static_cast<uint32_t*>(f);
+    k_zero_words<<<dim3(1), 64, 0, st>>>(reinterpret_cast<uint64_t*>(g_state[dev].fault), 1);
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    g_state_ready[dev].store(true, std::memory_order_release);
+  }
+  return &g_state[dev];
+}
+
+uint32_t wait_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+
+uint32_t* device_fault_word(hipStream_t st) {
+  const DeviceState* ds = device_state(st);
+  return ds ? ds->fault : nullptr;
+}
+
+// one single-launch reduction: kFusedLaunched, kFusedNotCovered or kFusedNoRoom
+inline int fused_dispatch(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
+                          const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles,
+                          void* workspace, size_t workspace_bytes, hipStream_t st) {
+#define FUSED_PASS ndim, in_shape, in_strides, axis, axis_len, out_size, tiles, workspace, workspace_bytes, st
+#define FUSED_CASE(T)                                                                                              \
+  {                                                                                                                \
+    const T* x = static_cast<const T*>(a);                                                                         \
+    T* cv = static_cast<T*>(c);                                                                                    \
+    int64_t* ci = static_cast<int64_t*>(c);                                                                        \
+    switch (op) {                                                                                                  \
+      case MUSAPY_RED_SUM: return launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), FUSED_PASS);          \
+      case MUSAPY_RED_PROD: return launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), FUSED_PASS);       \
+      case MUSAPY_RED_MAX:                                                                                         \
+        return launch_reduce_fused<OpMax<T>, OpExt<T, true, false, int64_t>, T>(x, vout<T>(cv), FUSED_PASS);       \
+      case MUSAPY_RED_MIN:                                                                                         \
+        return launch_reduce_fused<OpMin<T>, OpExt<T, false, false, int64_t>, T>(x, vout<T>(cv), FUSED_PASS);      \
+      case MUSAPY_RED_MEAN:                                                                                        \
+        if (sizeof(T) == 8 && T(0.5) == T(0)) return kFusedNotCovered; /* integer means go through f64 */          \
+        return launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, mean_count<T>(axis_len)), FUSED_PASS);    \
+      case MUSAPY_RED_ARGMAX: return launch_reduce_fused<OpArgmax<T>, OpArgmax64<T>, T>(x, iout<T>(ci), FUSED_PASS); \
+      case MUSAPY_RED_ARGMIN: return launch_reduce_fused<OpArgmin<T>, OpArgmin64<T>, T>(x, iout<T>(ci), FUSED_PASS); \
+    }                                                                                                              \
+    return kFusedNotCovered;                                                                                       \
+  }
+  // complex: sum, prod and mean (accumulated in f64 components, narrowed once; the mean divides by
+  // the f64 axis length, cpu_reduce_cplx, op_builder.rs:3485-3488)
+#define FUSED_CPLX(T)                                                                                              \
+  {                                                                                                                \
+    const T* x = static_cast<const T*>(a);                                                                         \
+    T* cv = static_cast<T*>(c);                                                                                    \
+    switch (op) {                                                                                                  \
+      case MUSAPY_RED_SUM: return launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), FUSED_PASS);          \
+      case MUSAPY_RED_PROD: return launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), FUSED_PASS);       \
+      case MUSAPY_RED_MEAN:                                                                                        \
+        return launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, double(axis_len)), FUSED_PASS);           \
+    }                                                                                                              \
+    return kFusedNotCovered;                                                                                       \
+  }
+  switch (dtype) {
+    case MUSAPY_DT_F32: FUSED_CASE(float)
+    case MUSAPY_DT_F64: FUSED_CASE(double)
+    case MUSAPY_DT_I64: FUSED_CASE(int64_t)
+    case MUSAPY_DT_C64: FUSED_CPLX(musapy_c64_t)
+    case MUSAPY_DT_C128: FUSED_CPLX(musapy_c128_t)
+  }
+#undef FUSED_CASE
+#undef FUSED_CPLX
+#undef FUSED_PASS
+  return kFusedNotCovered;
+}
 }  // namespace mpy
 
 #define RED_ARGS int ndim, const size_t *in_shape, const ssize_t *in_strides, int axis, size_t axis_len, size_t out_size
@@ -1031,78 +1165,43 @@ MPY_RED_ARG(argmin, OpArgmin, f64, double)
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
                            const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles,
                            void* workspace, size_t workspace_bytes, hipStream_t st) {
-#define FUSED_CASE(T)                                                                                           \
-  {                                                                                                             \
-    const T* x = static_cast<const T*>(a);                                                                      \
-    T* cv = static_cast<T*>(c);                                                                                 \
-    int64_t* ci = static_cast<int64_t*>(c);                                                                     \
-    bool ok = false;                                                                                            \
-    switch (op) {                                                                                               \
-      case MUSAPY_RED_SUM:                                                                                      \
-        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,             \
-                                                        workspace_bytes, st);                                   \
-        break;                                                                                                  \
-      case MUSAPY_RED_PROD:                                                                                     \
-        ok = launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,           \
-                                                          workspace_bytes, st);                                 \
-        break;                                                                                                  \
-      case MUSAPY_RED_MAX:                                                                                      \
-        ok = launch_reduce_fused<OpMax<T>, OpExt<T, true, false, int64_t>, T>(x, vout<T>(cv), RED_PASS, tiles,  \
-                                                                              workspace, workspace_bytes, st);  \
-        break;                                                                                                  \
-      case MUSAPY_RED_MIN:                                                                                      \
-        ok = launch_reduce_fused<OpMin<T>, OpExt<T, false, false, int64_t>, T>(x, vout<T>(cv), RED_PASS, tiles, \
-                                                                               workspace, workspace_bytes, st); \
-        break;                                                                                                  \
-      case MUSAPY_RED_MEAN:                                                                                     \
-        if (sizeof(T) == 8 && T(0.5) == T(0)) break; /* integer means go through f64 */                         \
-        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, mean_count<T>(axis_len)), RED_PASS,      \
-                                                        tiles, workspace, workspace_bytes, st);                 \
-        break;                                                                                                  \
-      case MUSAPY_RED_ARGMAX:                                                                                   \
-        ok = launch_reduce_fused<OpArgmax<T>, OpArgmax64<T>, T>(x, iout<T>(ci), RED_PASS, tiles, workspace,     \
-                                                                workspace_bytes, st);                           \
-        break;                                                                                                  \
-      case MUSAPY_RED_ARGMIN:                                                                                   \
-        ok = launch_reduce_fused<OpArgmin<T>, OpArgmin64<T>, T>(x, iout<T>(ci), RED_PASS, tiles, workspace,     \
-                                                                workspace_bytes, st);                           \
-        break;                                                                                                  \
-    }                                                                                                           \
-    return ok ? 0 : -1;                                                                                         \
-  }
-  // complex: sum, prod and mean (accumulated in f64 components, narrowed once; the mean divides by
-  // the f64 axis length, cpu_reduce_cplx, op_builder.rs:3485-3488)
-#define FUSED_CPLX(T)                                                                                           \
-  {                                                                                                             \
-    const T* x = static_cast<const T*>(a);                                                                      \
-    T* cv = static_cast<T*>(c);                                                                                 \
-    bool ok = false;                                                                                            \
-    switch (op) {                                                                                               \
-      case MUSAPY_RED_SUM:                                                                                      \
-        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,             \
-                                                        workspace_bytes, st);                                   \
-        break;                                                                                                  \
-      case MUSAPY_RED_PROD:                                                                                     \
-        ok = launch_reduce_fused<OpProd<T>, OpProd<T>, T>(x, vout<T>(cv), RED_PASS, tiles, workspace,           \
-                                                          workspace_bytes, st);                                 \
-        break;                                                                                                  \
-      case MUSAPY_RED_MEAN:                                                                                     \
-        ok = launch_reduce_fused<OpSum<T>, OpSum<T>, T>(x, mout<T>(cv, double(axis_len)), RED_PASS, tiles,      \
-                                                        workspace, workspace_bytes, st);                        \
-        break;                                                                                                  \
-    }                                                                                                           \
-    return ok ? 0 : -1;                                                                                         \
-  }
-  switch (dtype) {
-    case MUSAPY_DT_F32: FUSED_CASE(float)
-    case MUSAPY_DT_F64: FUSED_CASE(double)
-    case MUSAPY_DT_I64: FUSED_CASE(int64_t)
-    case MUSAPY_DT_C64: FUSED_CPLX(musapy_c64_t)
-    case MUSAPY_DT_C128: FUSED_CPLX(musapy_c128_t)
-  }
-#undef FUSED_CASE
-#undef FUSED_CPLX
-  return -1;
+  const int r = fused_dispatch(op, dtype, a, c, RED_PASS, tiles, workspace, workspace_bytes, st);
+  return r == kFusedLaunched ? 0 : -1;
 }
+
+// Returns and clears the device's wait-fault word (kFaultReduceWait | kFaultScanWait), read after
+// the caller has synchronized the streams whose work it covers.
+int musapy_kernels_take_fault(int device) {
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return -1;
+  if (device != prev && hipSetDevice(device) != hipSuccess) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  int result = 0;
+  const DeviceState* ds = device_state(nullptr);
+  if (ds == nullptr) {
+    result = -1;
+  } else {
+    uint32_t v = 0;
+    if (hipMemcpy(&v, ds->fault, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) {
+      result = -1;
+    } else if (v != 0) {
+      const uint32_t zero = 0;
+      if (hipMemcpy(ds->fault, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess)
+        result = -1;
+      else
+        result = int(v);
+    }
+  }
+  if (result < 0) (void)hipGetLastError();
+  if (device != prev) hipSetDevice(prev);
+  return result;
+}
+
+// Sets how many polls a bounded device wait makes before it gives up and reports a fault; returns
+// the previous limit.  0 makes every wait give up at once (used by tests to force the error path
+// while every kernel still exits normally).
+uint32_t musapy_kernels_set_spin_limit(uint32_t polls) { return g_spin_limit.exchange(polls); }
 
 }  // extern "C"

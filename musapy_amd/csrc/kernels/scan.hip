@@ -57,8 +57,8 @@ struct RowScanArgs {
   uint32_t tiles;       // tiles per row
   uint32_t* counter;    // tile claim counter; nullptr when tiles == 1 (no look-back)
   uint64_t* status;     // per row: inclusive prefixes of tiles 0..T-2, aggregates of 1..T-2
-  uint32_t* err;        // set when a look-back wait exceeds its bound
-  uint32_t spin_limit;
+  uint32_t* fault;      // the device's fault word (kcommon.hpp): a look-back wait ran out
+  uint32_t spin_limit;  // polls a look-back may make
   bool vec;             // 16-byte aligned rows
 };
 
@@ -157,6 +157,10 @@ __global__ __launch_bounds__(kSBlock) void k_scan_rows(const T* __restrict__ a, 
         bool ok = true;
         uint64_t b = 0;
         for (;;) {
+          if (spins++ >= sa.spin_limit) {  // a limit of 0 gives up before the first poll
+            ok = false;
+            break;
+          }
           if (read_value<W>(incl_of(j), b)) {
             P = from_bits<A>(b);
             break;
@@ -165,14 +169,10 @@ __global__ __launch_bounds__(kSBlock) void k_scan_rows(const T* __restrict__ a, 
             --j;
             continue;
           }
-          if (++spins > sa.spin_limit) {
-            ok = false;
-            break;
-          }
           __builtin_amdgcn_s_sleep(1);
         }
         if (!ok) {
-          atomicOr(sa.err, 1u);
+          atomicOr(sa.fault, kFaultScanWait);  // the prefix stays 0: the host reports the fault
         } else {
           // re-fold the aggregates after j in order: P(m) = P(m-1) + A(m)
           for (uint32_t m = j + 1; m < chunk; ++m) {
@@ -323,6 +323,14 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
   if (!args_ok(ndim, axis)) return;
   ScanPlan p;
   plan_scan(p, ndim, shape, strides, axis);
+  // rows and the non-axis extents are decoded in 32 bits (row_offsets, the lane index of
+  // k_scan_seq): refuse shapes past that instead of aliasing rows
+  bool fits = p.rows < (uint64_t(1) << 32);
+  for (int d = 0; d < p.ond; ++d) fits = fits && p.oshape[d] < (uint64_t(1) << 32);
+  if (!fits) {
+    g_wrapper_error = 4;
+    return;
+  }
   constexpr uint64_t TILE = uint64_t(kSBlock) * scan_items<T>();
   if (p.kind == kRowScan && p.L > 16) {
     RowScanArgs sa{};
@@ -338,7 +346,6 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
     sa.L = p.L;
     sa.rows = uint32_t(p.rows);
     sa.tiles = uint32_t((p.L + TILE - 1) / TILE);
-    sa.spin_limit = 1u << 24;
     bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c)) & 15u) == 0;
     for (int d = 0; d < p.ond; ++d)
       if (((p.istride[d] * int64_t(sizeof(T))) % 16) || ((p.ostride[d] * int64_t(sizeof(T))) % 16)) vec = false;
@@ -356,9 +363,13 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
       uint64_t bpr = (p.L + 255) / 256;
       uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
       // word 0: claim counter; then per row (2*tiles-3)*W status words (inclusive prefixes of
-      // tiles 0..T-2, aggregates of tiles 1..T-2); last word: error flag
+      // tiles 0..T-2, aggregates of tiles 1..T-2); one spare word
       const uint64_t W = sizeof(T) == 4 ? 1 : 2;
       uint64_t words = 2 + uint64_t(p.rows) * (2 * uint64_t(sa.tiles) - 3) * W;
+      if (uint64_t(p.rows) * sa.tiles >= (uint64_t(1) << 32)) {  // tile ids are 32-bit
+        g_wrapper_error = 4;
+        return;
+      }
       if (tmp == nullptr || words * 8 > cap) {
         g_wrapper_error = 1;
         return;
@@ -366,7 +377,12 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
       uint64_t* w = reinterpret_cast<uint64_t*>(tmp);
       sa.counter = reinterpret_cast<uint32_t*>(w);
       sa.status = w + 1;
-      sa.err = reinterpret_cast<uint32_t*>(w + words - 1);
+      sa.fault = device_fault_word(st);
+      sa.spin_limit = wait_spin_limit();
+      if (sa.fault == nullptr) {  // a wait that ran out could not be reported: take no waits
+        g_wrapper_error = 1;
+        return;
+      }
       unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
       k_scan_clear<<<cg, 256, 0, st>>>(w, words);
     }

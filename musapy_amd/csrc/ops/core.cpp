@@ -7,6 +7,7 @@
 #include <mutex>
 
 #include "../../../include/musapy_hip_runtime.h"
+#include "../../../include/musapy_kernels.h"
 
 namespace mpy {
 namespace ops {
@@ -249,7 +250,27 @@ void Stream::synchronize() {
     poisoned_ = true;
     throw StreamError(std::string("stream synchronize failed: ") + mpy_rt_error_string(code));
   }
-  if (poisoned_) throw StreamError("stream is poisoned by an earlier failure");
+  if (!wait_check_) return;
+  wait_check_ = false;
+  const int fault = musapy_kernels_take_fault(device_);
+  if (fault == 0) return;
+  poisoned_ = true;
+  if (fault < 0) throw StreamError("stream synchronize: the device's wait-fault word could not be read");
+  // A producer that published after its combiner gave up left a tagged slot: start clean.
+  if (workspace_) {
+    int c2 = mpy_rt_fill_u32(workspace_, 0u, kReduceWorkspaceBytes, raw_);
+    if (c2 == 0) c2 = mpy_rt_stream_synchronize(raw_);
+    if (c2 != 0) {
+      mpy_rt_free(workspace_, raw_);  // never reuse slots that may be stale
+      workspace_ = nullptr;
+    }
+  }
+  std::string what;
+  if (fault & 1) what += "a single-launch reduction's combiner";
+  if (fault & 2) what += std::string(what.empty() ? "" : " and ") + "a cumsum look-back";
+  throw KernelError("device wait expired in " + what +
+                    ": results of the work queued on this stream since its last synchronize are invalid "
+                    "(stream poisoned)");
 }
 
 StreamPtr Stream::create(int device) {

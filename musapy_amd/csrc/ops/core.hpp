@@ -86,8 +86,14 @@ class Stream {
   uint64_t id() const { return id_; }
   bool is_poisoned() const { return poisoned_; }
   void poison() { poisoned_ = true; }
-  // synchronize; a failure poisons the stream and raises StreamError (stream.rs:311-377)
+  // Synchronize (stream.rs:311-377).  A failing synchronize poisons the stream and raises
+  // StreamError.  When work with a bounded device wait (note_bounded_wait) was queued since the
+  // last synchronize, the device's wait-fault word is read as well: a wait that ran out poisons
+  // the stream, re-zeroes its reduction workspace and raises KernelError.  As in the reference,
+  // poison is a mark (is_poisoned), not a refusal of later work.
   void synchronize();
+  // the op layer queued a kernel whose waits can run out (single-launch reduction, row scan)
+  void note_bounded_wait() { wait_check_ = true; }
   static std::shared_ptr<Stream> create(int device);
   // The priority a caller asked for (stream.rs:154-199).  It is recorded, not applied: every
   // stream of this backend runs at the default priority.
@@ -104,6 +110,7 @@ class Stream {
   hipStream_t raw_;
   bool owned_;
   bool poisoned_ = false;
+  bool wait_check_ = false;
   uint64_t id_;
   int priority_ = 0;
   void* workspace_ = nullptr;

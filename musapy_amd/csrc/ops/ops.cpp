@@ -560,8 +560,11 @@ bool red_fused(ReduceKernel k, Dtype ct, const RedCall& c, void* out, size_t til
     case Dtype::Complex128: dt = MUSAPY_DT_C128; break;
     default: return false;
   }
-  return musapy_reduce_fused_v1(op, dt, c.a, out, c.nd, c.shape, c.strides, c.axis, c.axis_len, c.out_size, tiles,
-                                s.reduce_workspace(), Stream::kReduceWorkspaceBytes, c.s) == 0;
+  if (musapy_reduce_fused_v1(op, dt, c.a, out, c.nd, c.shape, c.strides, c.axis, c.axis_len, c.out_size, tiles,
+                             s.reduce_workspace(), Stream::kReduceWorkspaceBytes, c.s) != 0)
+    return false;
+  s.note_bounded_wait();
+  return true;
 }
 
 // partial -> final for value reductions (sum/prod/max/min/mean)
@@ -823,6 +826,7 @@ Array cumsum_op(const Array& a, std::optional<size_t> axis, const Array* out) {
     if (bpr > 1) tmp = Buffer::alloc(scratch * element_size(ct), a.device, s);
     void* tp = tmp ? tmp->ptr() : nullptr;
     const int nd = int(kshape.size());
+    s->note_bounded_wait();  // row scans split into tiles wait on their predecessors
     if (ct == Dtype::Int64)
       musapy_cumsum_i64_v3((const int64_t*)aw->data_ptr(), (int64_t*)r.data_ptr(), (int64_t*)tp, nd, kshape.data(),
                            kstrides.data(), kaxis, axis_len, out_size, s->raw());

@@ -277,6 +277,8 @@ const char* mpy_rt_error_string(int code) {
   if (code == -1) return "kernel wrapper error: cumsum scratch buffer missing or too small";
   if (code == -2) return "kernel wrapper error: a reduction tile reaches 2^31 elements (pass more tiles)";
   if (code == -3) return "kernel wrapper error: ndim outside [0, 32] or axis outside [0, ndim)";
+  if (code == -4) return "kernel wrapper error: a cumsum with 2^32 or more rows (or a non-axis extent of 2^32 or more)";
+  if (code == -5) return "kernel wrapper error: the reduction needs more scratch than the no-alloc entry point holds";
   if (code < 0) return "kernel wrapper error";
   return hipGetErrorString(hipError_t(code));
 }

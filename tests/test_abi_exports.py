@@ -13,7 +13,7 @@ HEADERS = [os.path.join(ROOT, "include", h) for h in ("musapy_kernels.h", "musap
 def declared(path):
     text = open(path).read()
     text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
-    return re.findall(r"^\s*(?:void|int|size_t|const char\*)\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:void|int|size_t|uint32_t|const char\*)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 def test_headers_declare_the_hot_path():

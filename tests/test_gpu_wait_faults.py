@@ -1,0 +1,137 @@
+"""Bounded device waits that run out are reported, not folded into a wrong result.
+
+The combiner of a single-launch reduction and the look-back of a tiled row scan wait for other
+workgroups.  Each wait polls a bounded number of times; `musapy_kernels_set_spin_limit(0)` makes
+every such wait give up before its first poll, so the error path runs while every kernel still
+exits normally (nothing here makes the GPU fault or hang).  Expected behaviour, as the reference
+surfaces execution errors at stream synchronisation (rust/musapy-core/src/stream.rs:311-377):
+the synchronize that covers the work raises KernelError and poisons the stream, and the next
+reduction on that stream is correct again.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import musapy_amd as ms
+from oracle import reference as R
+from tests.conftest import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "musapy_amd", "libmusapy_hip.so")
+RNG = np.random.default_rng(41)
+
+
+def _lib():
+    lib = ctypes.CDLL(LIB)
+    lib.musapy_kernels_set_spin_limit.restype = ctypes.c_uint32
+    lib.musapy_kernels_set_spin_limit.argtypes = [ctypes.c_uint32]
+    lib.musapy_kernels_take_fault.restype = ctypes.c_int
+    lib.musapy_kernels_take_fault.argtypes = [ctypes.c_int]
+    return lib
+
+
+class _NoPolls:
+    """Every bounded wait gives up at once while inside the block."""
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    def __enter__(self):
+        self.prev = self.lib.musapy_kernels_set_spin_limit(0)
+        return self
+
+    def __exit__(self, *exc):
+        self.lib.musapy_kernels_set_spin_limit(self.prev)
+
+
+def _fresh_stream_case(make, run, check):
+    """Runs `run` on its own stream with no polls allowed, expects KernelError at the readback,
+    then runs it again with the default limit and checks the result."""
+    lib = _lib()
+    s = ms.Stream()
+    with ms.stream(s):
+        inputs = make()
+        good = run(*inputs).numpy()  # the normal path first
+        check(good, "before the forced fault")
+        with _NoPolls(lib):
+            bad = run(*inputs)
+            with pytest.raises(ms.KernelError, match="device wait expired"):
+                bad.numpy()
+        assert s.is_poisoned
+        again = run(*inputs).numpy()  # same stream, default limit again
+        check(again, "after the forced fault")
+        assert_bits_equal(again, good, "rerun on the recovered stream")
+    assert lib.musapy_kernels_take_fault(0) == 0  # the fault was consumed by the readback
+
+
+def test_whole_array_reduction_gives_up_and_recovers():
+    x = RNG.standard_normal(1 << 22).astype(np.float32)
+    want = R.reduce(x, "sum", None)
+
+    def check(got, what):
+        assert abs(float(got) - float(want)) <= 1e-5 * np.abs(x).sum(), what
+
+    _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X: ms.sum(X), check)
+    _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X: ms.argmax(X),
+                       lambda got, what: assert_bits_equal(got, R.reduce(x, "argmax", None), what))
+
+
+def test_row_reduction_gives_up_and_recovers():
+    x = RNG.standard_normal((8, 1 << 20)).astype(np.float32)
+    _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X: ms.argmax(X, axis=1),
+                       lambda got, what: assert_bits_equal(got, R.reduce(x, "argmax", 1), what))
+    _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X: ms.max(X, axis=1),
+                       lambda got, what: assert_bits_equal(got, R.reduce(x, "max", 1), what))
+
+
+def test_row_scan_look_back_gives_up_and_recovers():
+    y = RNG.random((4, 100_000))
+    want = R.cumsum(y, 1)
+
+    def check(got, what):
+        assert np.all(np.abs(got - want) <= 1e-12 * np.abs(want)), what
+
+    _fresh_stream_case(lambda: (ms.from_numpy(y),), lambda Y: ms.cumsum(Y, axis=1), check)
+
+
+def test_c_abi_fault_word_and_workspace_reuse():
+    """A caller of musapy_reduce_fused_v1 reads the fault with musapy_kernels_take_fault after its
+    synchronize, zeroes its workspace, and the next call is correct."""
+    lib = _lib()
+    P, I, SZ, SS = ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_ssize_t)
+    lib.musapy_reduce_fused_v1.restype = ctypes.c_int
+    lib.musapy_reduce_fused_v1.argtypes = [I, I, P, P, I, SZ, SS, I, ctypes.c_size_t, ctypes.c_size_t,
+                                           ctypes.c_size_t, P, ctypes.c_size_t, P]
+    RED_SUM, DT_F64 = 0, 11
+    x = RNG.standard_normal((4, 1 << 18))
+    X = ms.from_numpy(x)
+    C = ms.from_numpy(np.zeros(4))
+    ws_words = 4 * 64 * 2
+    WS = ms.from_numpy(np.zeros(ws_words, np.uint64))
+    shape = (ctypes.c_size_t * 2)(4, 1 << 18)
+    strides = (ctypes.c_ssize_t * 2)(1 << 18, 1)
+    ms.synchronize()
+    assert lib.musapy_kernels_take_fault(0) == 0
+
+    def call():
+        return lib.musapy_reduce_fused_v1(RED_SUM, DT_F64, X.data_ptr, C.data_ptr, 2, shape, strides, 1, 1 << 18, 4,
+                                          64, WS.data_ptr, ws_words * 8, X.stream_ptr)
+
+    with _NoPolls(lib):
+        assert call() == 0
+        ms.synchronize()
+    assert lib.musapy_kernels_take_fault(0) == 1
+    assert lib.musapy_kernels_take_fault(0) == 0  # taking it clears it
+    WS2 = ms.from_numpy(np.zeros(ws_words, np.uint64))  # a late publisher may have left tags in WS
+    ms.synchronize()
+    assert lib.musapy_reduce_fused_v1(RED_SUM, DT_F64, X.data_ptr, C.data_ptr, 2, shape, strides, 1, 1 << 18, 4, 64,
+                                      WS2.data_ptr, ws_words * 8, X.stream_ptr) == 0
+    ms.synchronize()
+    assert lib.musapy_kernels_take_fault(0) == 0
+    got = C.numpy()
+    want = R.reduce(x, "sum", 1)
+    assert np.all(np.abs(got - want) <= 1e-12 * np.abs(x).sum(axis=1))
+    assert not WS2.numpy().any(), "the workspace is left zero"
