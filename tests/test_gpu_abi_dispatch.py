@@ -331,7 +331,12 @@ def test_cumsum_with_reference_scratch(dt):
             what = f"cumsum {np.dtype(dt).name} {view.shape} {view.strides} axis={ax}"
             if dt == np.int64:
                 assert_bits_equal(got, want, what)
-            else:
-                tol = 1e-5 if dt == np.float32 else 1e-12
-                bound = tol * np.cumsum(np.abs(view.astype(np.float64)), axis=ax)
-                assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-30), what
+                continue
+            tol = 1e-5 if dt == np.float32 else 1e-12
+            bound = tol * np.cumsum(np.abs(view.astype(np.float64)), axis=ax)
+            if dt == np.float32 and L > 65536:
+                # The reference's sequential f32 running sum itself drifts by about sqrt(L) * eps
+                # * sum|x| (3e-5 relative at L = 300,000 on U(0,1) data), more than the bound; no
+                # order of additions can follow it, so this case is held to the exact prefix sums.
+                want = np.cumsum(view.astype(np.float64), axis=ax)
+            assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-30), what
