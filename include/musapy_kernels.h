@@ -324,13 +324,26 @@ enum { MUSAPY_RED_SUM = 0, MUSAPY_RED_PROD, MUSAPY_RED_MAX, MUSAPY_RED_MIN, MUSA
        MUSAPY_RED_ARGMIN };
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---- single-launch reduction that allocates nothing (new; no counterpart in kernels.rs) ----
+ * For callers that cannot call hipMalloc: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  Same operation, arguments and results as
+ * musapy_reduce_fused_v1, without `workspace`: the slots live in a static 1 MiB device array of
+ * the library (one per GPU, held until the process ends; zeroed by the first call on a device,
+ * left zero by every call).  The caller still passes the input and the output.  Returns 0 when
+ * launched, -1 when the case is not covered (nothing launched), -2 when its slots need more than
+ * the 1 MiB the array holds (out_size * tiles * W words of 8 bytes, W as above; nothing
+ * launched, wrapper error 5).  Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (concurrent streams or host threads) race and must be ordered by the caller. */
+int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, hipStream_t stream);
+
 /* ---- wrapper-level error (new; no counterpart in kernels.rs) ----
  * Returns and clears the calling thread's last wrapper error: 0 none, 1 a cumsum scratch buffer
  * that is NULL or smaller than the reference's scratch formula requires, 2 a reduction whose
  * per-tile length reaches 2^31 elements (pass more tiles), 3 ndim outside [0, 32] or an axis
  * outside [0, ndim) (32 is the reference's MUSAPY_MAX_NDIM), 4 a cumsum with 2^32 or more rows
- * (or a dimension outside the scanned axis of 2^32 or more).  A wrapper that reports an error
- * launches nothing. */
+ * (or a dimension outside the scanned axis of 2^32 or more), 5 a no-alloc reduction whose slots
+ * need more than the library's static scratch.  A wrapper that reports an error launches
+ * nothing. */
 int musapy_kernels_take_error(void);
 
 /* ---- device wait faults (new; no counterpart in kernels.rs) ----

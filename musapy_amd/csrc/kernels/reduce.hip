@@ -939,14 +939,18 @@ template <class T> using OpArgmax64 = OpExt<T, true, true, int64_t>;  // over (v
 template <class T> using OpArgmin64 = OpExt<T, false, true, int64_t>;
 
 // --------------------------------------------------------------------------------------------
-// Device-resident state of the library: the fault word of the bounded waits.  Each GPU the
-// library runs on holds its own copy until the process ends.  In host code the variable's name is
-// a host-side stand-in, not a device address: the kernels are only ever given the address that
-// hipGetSymbolAddress returns for the current device (DeviceState).
+// Device-resident state of the library: the fault word of the bounded waits, and `scratch`, the
+// workspace of the no-alloc single-launch reduction (musapy_reduce_fused_noalloc_v1).  Each GPU
+// the library runs on holds its own copy of both until the process ends.  In host code the
+// names are host-side stand-ins, not device addresses: kernels and copies are only ever given
+// the addresses that hipGetSymbolAddress returns for the current device (DeviceState).
+constexpr size_t kScratchBytes = size_t(1) << 20;  // 1 MiB: out_size * tiles * W <= 131072 words
+static __device__ __align__(256) uint64_t scratch[kScratchBytes / 8];
 static __device__ __align__(256) uint32_t wait_fault;
 
 constexpr int kMaxDevices = 64;
 struct DeviceState {
+  uint64_t* scratch;  // device address of `scratch` on this device
   uint32_t* fault;    // device address of `wait_fault` on this device
 };
 std::mutex g_state_mu;
@@ -960,8 +964,8 @@ __global__ void k_zero_words(uint64_t* w, uint64_t n) {
 }
 
 // The current device's state, resolved once per device with that device current.  The first call
-// on a device also zeroes the fault word with a kernel on `st` (ordered before the caller's work
-// on that stream).  nullptr when a HIP call fails.
+// on a device also zeroes both arrays with kernels on `st` (ordered before the caller's work on
+// that stream).  nullptr when a HIP call fails.
 const DeviceState* device_state(hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
@@ -971,12 +975,16 @@ const DeviceState* device_state(hipStream_t st) {
   if (g_state_ready[dev].load(std::memory_order_acquire)) return &g_state[dev];
   std::lock_guard<std::mutex> lk(g_state_mu);
   if (!g_state_ready[dev].load(std::memory_order_relaxed)) {
+    void* s = nullptr;
     void* f = nullptr;
-    if (hipGetSymbolAddress(&f, HIP_SYMBOL(wait_fault)) != hipSuccess || f == nullptr) {
+    if (hipGetSymbolAddress(&s, HIP_SYMBOL(scratch)) != hipSuccess || s == nullptr ||
+        hipGetSymbolAddress(&f, HIP_SYMBOL(wait_fault)) != hipSuccess || f == nullptr) {
       (void)hipGetLastError();
       return nullptr;
     }
+    g_state[dev].scratch = static_cast<uint64_t*>(s);
     g_state[dev].fault = static_cast<uint32_t*>(f);
+    k_zero_words<<<dim3(256), 256, 0, st>>>(g_state[dev].scratch, kScratchBytes / 8);
     k_zero_words<<<dim3(1), 64, 0, st>>>(reinterpret_cast<uint64_t*>(g_state[dev].fault), 1);
     if (hipGetLastError() != hipSuccess) return nullptr;
     g_state_ready[dev].store(true, std::memory_order_release);
@@ -1169,8 +1177,25 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
   return r == kFusedLaunched ? 0 : -1;
 }
 
+// The same single launch with the library's static scratch as its workspace (new; no counterpart
+// in kernels.rs): for callers that cannot allocate.  Calls that overlap on one device race.
+int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
+                                   const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size,
+                                   size_t tiles, hipStream_t st) {
+  const DeviceState* ds = device_state(st);
+  if (ds == nullptr) return -1;
+  const int r = fused_dispatch(op, dtype, a, c, RED_PASS, tiles, ds->scratch, kScratchBytes, st);
+  if (r == kFusedNoRoom) {
+    g_wrapper_error = 5;
+    return -2;
+  }
+  return r == kFusedLaunched ? 0 : -1;
+}
+
 // Returns and clears the device's wait-fault word (kFaultReduceWait | kFaultScanWait), read after
-// the caller has synchronized the streams whose work it covers.
+// the caller has synchronized the streams whose work it covers.  When a fault is found, the
+// static scratch is cleared as well (a publisher that finished after its combiner gave up may
+// have left a tag in it).
 int musapy_kernels_take_fault(int device) {
   int prev = 0;
   if (hipGetDevice(&prev) != hipSuccess) return -1;
@@ -1188,7 +1213,8 @@ int musapy_kernels_take_fault(int device) {
       result = -1;
     } else if (v != 0) {
       const uint32_t zero = 0;
-      if (hipMemcpy(ds->fault, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess)
+      if (hipMemcpy(ds->fault, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess ||
+          hipMemset(ds->scratch, 0, kScratchBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
         result = -1;
       else
         result = int(v);
