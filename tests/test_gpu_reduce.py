@@ -383,3 +383,27 @@ def test_column_reductions_split_into_row_tiles(kind, dt):
                 flat[0, ::7] = np.nan   # NaN at axis position 0 absorbs those columns
                 flat[3, 1::5] = np.nan  # later NaNs are skipped
         check_reduce(kind, x, ax)
+
+
+def test_cumsum_look_back_long_rows():
+    """Few long rows take the decoupled look-back over tiles claimed in memory order: a row of
+    2^24 f64 is 4096 tiles, so most tiles find their predecessor's prefix beyond the 64-tile window
+    and wait for it to move; int64 is exact, floats within the prefix bound of the oracle and the
+    same bits on every run."""
+    for shape, dt in (((1, 1 << 24), np.float64), ((3, 5_000_001), np.int64), ((7, 300_001), np.float32),
+                      ((64, 65536), np.float64), ((2, 4097), np.float64), ((5, 8193), np.float32)):
+        x = RNG.integers(-1000, 1000, shape) if dt == np.int64 else RNG.random(shape)
+        x = x.astype(dt)
+        X = dev(x)
+        got = ms.cumsum(X, axis=1).numpy()
+        want = R.cumsum(x, 1)
+        what = f"look-back cumsum {np.dtype(dt).name} {shape}"
+        if dt == np.int64:
+            assert_bits_equal(got, want, what)
+        else:
+            exact = np.cumsum(x.astype(np.float64), axis=1)
+            bound = TOL[dt] * np.cumsum(np.abs(x.astype(np.float64)), axis=1)
+            if dt == np.float32:  # the sequential f32 reference drifts past the bound on long rows
+                bound = bound + np.abs(want - exact)
+            assert np.all(np.abs(got.astype(np.float64) - want) <= bound), what
+        assert_bits_equal(ms.cumsum(X, axis=1).numpy(), got, what + " run-to-run")
