@@ -7,16 +7,18 @@ that metric names:
     C4  sum      axis=-1 of an (8192, 8192) f32 N(0,1) array, seed 0   4 B/elem + 4 B/row
     C4  argmax   axis=1 of the same array -> int64                    4 B/elem + 8 B/row
 Inputs are resident in HBM before timing.  Each op is launched K times back-to-back between two
-HIP events on the stream it runs on, with outputs preallocated (out=) and the inputs rotated
-over 4 device copies, so every launch streams its inputs from HBM rather than from the 256 MB
-Infinity Cache.  `value` = algorithmic bytes of the step / summed average launch time.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
+HIP events on the stream it runs on, with outputs preallocated (out=) and inputs and outputs
+rotated over 4 device buffers, so every launch streams from HBM rather than from the 256 MB
+Infinity Cache.  `value` = algorithmic bytes of the step / summed average launch time.
+`mall_flushed` repeats the step with each launch timed alone after 768 MB of other traffic.  `cpu_baseline` times the CPU oracle (single-threaded C restatement of
 musapy's CPU path) on the same step.
 
-    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu] [--only add|sum|argmax|copy]
+    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu] [--only KEY]
 """
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import re
@@ -35,9 +37,10 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--all", action="store_true", help="also time every BASELINE config (table on stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--only", choices=["add", "sum", "argmax", "copy"],
-                   help="launch one step op (or the calibration copy) warmup+steps times and exit; "
-                        "the program run under rocprofv3 --pmc for the HBM traffic figures")
+    p.add_argument("--only", metavar="KEY",
+                   help="launch one op warmup+steps times and exit (a step op: add, sum, argmax; the "
+                        "calibration copy: copy; or a config key of --all, e.g. cumsum, max01): the "
+                        "program run under rocprofv3 --pmc for the HBM traffic figures")
     return p.parse_args()
 
 
@@ -73,12 +76,16 @@ class Timer:
     def run(self, launches):
         """Launches back-to-back between two events; returns the average launch time (ms).
         `host_ms` keeps the host time per launch of the same loop (the time to enqueue it)."""
-        self.t.start()
-        h0 = time.perf_counter()
-        for f in launches:
-            f()
-        self.host_ms = (time.perf_counter() - h0) * 1e3 / len(launches)
-        self.t.stop()
+        gc.disable()  # a collection inside the loop would stall the launches and idle the GPU
+        try:
+            self.t.start()
+            h0 = time.perf_counter()
+            for f in launches:
+                f()
+            self.host_ms = (time.perf_counter() - h0) * 1e3 / len(launches)
+            self.t.stop()
+        finally:
+            gc.enable()
         return self.t.elapsed_ms() / len(launches)
 
 
@@ -93,16 +100,19 @@ def step_ops(ms):
     b = rng.uniform(-1, 1, 16_777_216).astype(np.float32)
     x = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
     A, B, X = _copies(ms, a), _copies(ms, b), _copies(ms, x)
-    C = ms.from_numpy(np.zeros_like(a))
-    S = ms.from_numpy(np.zeros(8192, np.float32))
-    I = ms.from_numpy(np.zeros(8192, np.int64))
+    # outputs rotate over as many buffers as the inputs, so no launch writes the lines the previous
+    # one left in the Infinity Cache
+    C = [ms.from_numpy(np.zeros_like(a)) for _ in range(COPIES)]
+    S = [ms.from_numpy(np.zeros(8192, np.float32)) for _ in range(COPIES)]
+    I = [ms.from_numpy(np.zeros(8192, np.int64)) for _ in range(COPIES)]
     n = 8192 * 8192
     ops = [
-        ("add", "C1 add f32 16,777,216", lambda i: ms.add(A[i % COPIES], B[i % COPIES], out=C), 12 * 16_777_216),
-        ("sum", "C4 sum axis=-1 (8192,8192) f32", lambda i: ms.sum(X[i % COPIES], axis=-1, out=S),
+        ("add", "C1 add f32 16,777,216", lambda i: ms.add(A[i % COPIES], B[i % COPIES], out=C[i % COPIES]),
+         12 * 16_777_216),
+        ("sum", "C4 sum axis=-1 (8192,8192) f32", lambda i: ms.sum(X[i % COPIES], axis=-1, out=S[i % COPIES]),
          4 * n + 4 * 8192),
-        ("argmax", "C4 argmax axis=1 (8192,8192) f32", lambda i: ms.argmax(X[i % COPIES], axis=1, out=I),
-         4 * n + 8 * 8192),
+        ("argmax", "C4 argmax axis=1 (8192,8192) f32",
+         lambda i: ms.argmax(X[i % COPIES], axis=1, out=I[i % COPIES]), 4 * n + 8 * 8192),
     ]
     # calibration: a plain copy of a unit-stride view starting 4 KiB in (page- and line-aligned,
     # so no cache line is shared between workgroups): one vectorised copy kernel
@@ -114,12 +124,14 @@ def step_ops(ms):
 
 
 def all_config_ops(ms, host_legs=False):
-    """Every BASELINE config op (for the per-config table); inputs rotate over 3 copies.
+    """Every BASELINE config op (for the per-config table), built one at a time.
 
-    Rows are (name, gpu launch of launch index i, algorithmic bytes, cpu leg).  With `host_legs`
-    the BASELINE config rows carry a cpu leg: a function that runs the CPU oracle (the
+    Rows are (key, name, build).  build() uploads that op's inputs (3 copies, rotated between
+    launches) and returns (gpu launch of launch index i, algorithmic bytes, cpu leg).  With
+    `host_legs` the BASELINE config rows carry a cpu leg: a function that runs the CPU oracle (the
     single-threaded C restatement of musapy's CPU path) once on the same host inputs and returns
-    the algorithmic bytes it covered.  The widened rows carry none."""
+    the algorithmic bytes it covered.  The widened rows carry none.  `key` names the op for
+    `--only` (the program profiled under rocprofv3 --pmc)."""
     K = 3
     R = None
     if host_legs:
@@ -129,109 +141,250 @@ def all_config_ops(ms, host_legs=False):
     def leg(f, nbytes):
         return (lambda: (f(), nbytes)[1]) if R is not None else None
 
-    rng = np.random.default_rng(0)
-    ops = []
-    a64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
-    b64 = rng.uniform(-1, 1, 67_108_864).astype(np.float32)
-    A64, B64 = _copies(ms, a64, K), _copies(ms, b64, K)
-    ops.append(("C1-64M add f32 67,108,864", lambda i: ms.add(A64[i % K], B64[i % K]), 12 * 67_108_864,
-                leg(lambda: R.binary("add", a64, b64), 12 * 67_108_864)))
-    ops.append(("full sum f32 64M", lambda i: ms.sum(A64[i % K]), 4 * 67_108_864 + 4,
-                leg(lambda: R.reduce(a64, "sum"), 4 * 67_108_864 + 4)))
-    ops.append(("full argmax f32 64M", lambda i: ms.argmax(A64[i % K]), 4 * 67_108_864 + 8,
-                leg(lambda: R.reduce(a64, "argmax"), 4 * 67_108_864 + 8)))
-    # the same whole-array reductions at 4x the size: the fixed end-of-launch hand-over amortised
-    a256 = np.random.default_rng(1).uniform(-1, 1, 268_435_456).astype(np.float32)
-    A256 = _copies(ms, a256, K)
-    ops.append(("full sum f32 256M", lambda i: ms.sum(A256[i % K]), 4 * 268_435_456 + 4,
-                leg(lambda: R.reduce(a256, "sum"), 4 * 268_435_456 + 4)))
-    ops.append(("full argmax f32 256M", lambda i: ms.argmax(A256[i % K]), 4 * 268_435_456 + 8,
-                leg(lambda: R.reduce(a256, "argmax"), 4 * 268_435_456 + 8)))
-    r = np.random.default_rng(0)
-    ca, cb = r.uniform(-1, 1, (4096, 1)).astype(np.float32), r.uniform(-1, 1, (8192,)).astype(np.float32)
-    CA, CB = _copies(ms, ca, K), _copies(ms, cb, K)
-    nb = 4 * 33_554_432 + 4 * 4096 + 4 * 8192
-    ops.append(("C2 broadcast add (4096,1)+(8192,)", lambda i: ms.add(CA[i % K], CB[i % K]), nb,
-                leg(lambda: R.binary("add", ca, cb), nb)))
-    xh = np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32)
-    xt = [ms.transpose(c) for c in _copies(ms, xh, K)]
-    ops.append(("C2 exp transposed (8192,4096)^T", lambda i: ms.exp(xt[i % K]), 8 * 33_554_432,
-                leg(lambda: R.unary("exp", xh.T), 8 * 33_554_432)))
-    r = np.random.default_rng(0)
-    i64h = r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64)
-    f64h = r.standard_normal((2048, 2048, 4))
-    i64, f64 = _copies(ms, i64h, K), _copies(ms, f64h, K)
     N = 16_777_216
-    sh = i64h.astype(np.float64) + f64h  # the host inputs of the later C3 steps (values only feed timing)
-    ch = np.clip(sh, -1.0, 1.0)
-    fh = ch.astype(np.float32)
-    ops.append(("C3 add i64+f64->f64 (cast+add)", lambda i: ms.add(i64[i % K], f64[i % K]), 24 * N,
-                leg(lambda: R.binary("add", i64h, f64h), 24 * N)))
-    s = [ms.add(i64[k], f64[k]) for k in range(K)]
-    ops.append(("C3 clamp f64", lambda i: ms.clamp(s[i % K], -1.0, 1.0), 16 * N,
-                leg(lambda: R.clamp(sh, -1.0, 1.0), 16 * N)))
-    c = [ms.clamp(s[k], -1.0, 1.0) for k in range(K)]
-    ops.append(("C3 astype f64->f32", lambda i: ms.astype(c[i % K], "f32"), 12 * N,
-                leg(lambda: R.cast(ch, "f32"), 12 * N)))
-    f = [ms.astype(c[k], "f32") for k in range(K)]
-    ops.append(("C3 astype f32->bf16", lambda i: ms.astype(f[i % K], "bf16"), 6 * N,
-                leg(lambda: R.cast(fh, "bf16"), 6 * N)))
-    ops.append(("C3 astype f32->f16", lambda i: ms.astype(f[i % K], "f16"), 6 * N,
-                leg(lambda: R.cast(fh, "f16"), 6 * N)))
-    Xh = np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32)
-    X = _copies(ms, Xh, K)
+    M = 16 * 1024 * 1024
     n = 8192 * 8192
-    ops.append(("C4 sum axis=0", lambda i: ms.sum(X[i % K], axis=0), 4 * n + 4 * 8192,
-                leg(lambda: R.reduce(Xh, "sum", 0), 4 * n + 4 * 8192)))
-    ops.append(("C4 mean axis=-1", lambda i: ms.mean(X[i % K], axis=-1), 4 * n + 4 * 8192,
-                leg(lambda: R.reduce(Xh, "mean", -1), 4 * n + 4 * 8192)))
-    ops.append(("C4 mean axis=0", lambda i: ms.mean(X[i % K], axis=0), 4 * n + 4 * 8192,
-                leg(lambda: R.reduce(Xh, "mean", 0), 4 * n + 4 * 8192)))
-    ops.append(("C4 max axis=(0,1)", lambda i: ms.max(X[i % K], axis=(0, 1)), 4 * n + 4,
-                leg(lambda: R.reduce(Xh, "max", (0, 1)), 4 * n + 4)))
-    ops.append(("C4 argmin axis=1", lambda i: ms.argmin(X[i % K], axis=1), 4 * n + 8 * 8192,
-                leg(lambda: R.reduce(Xh, "argmin", 1), 4 * n + 8 * 8192)))
-    yh = np.random.default_rng(0).random((1024, 65536))
-    y = _copies(ms, yh, K)
-    ops.append(("C5 cumsum f64 (1024,65536) axis=1", lambda i: ms.cumsum(y[i % K], axis=1), 16 * 1024 * 65536,
-                leg(lambda: R.cumsum(yh, axis=1), 16 * 1024 * 65536)))
-    if R is not None:
+    cache = {}
+
+    def get(name, make):
+        if name not in cache:
+            cache[name] = make()
+        return cache[name]
+
+    def a64():
+        return get("a64", lambda: np.random.default_rng(0).uniform(-1, 1, 67_108_864).astype(np.float32))
+
+    def b64():
+        def mk():
+            r = np.random.default_rng(0)
+            r.uniform(-1, 1, 67_108_864)
+            return r.uniform(-1, 1, 67_108_864).astype(np.float32)
+        return get("b64", mk)
+
+    def a256():
+        return get("a256", lambda: np.random.default_rng(1).uniform(-1, 1, 268_435_456).astype(np.float32))
+
+    def c2():
+        def mk():
+            r = np.random.default_rng(0)
+            return r.uniform(-1, 1, (4096, 1)).astype(np.float32), r.uniform(-1, 1, (8192,)).astype(np.float32)
+        return get("c2", mk)
+
+    def c3():
+        def mk():
+            r = np.random.default_rng(0)
+            i64h = r.integers(-1000, 1001, (2048, 2048, 4), dtype=np.int64)
+            f64h = r.standard_normal((2048, 2048, 4))
+            sh = i64h.astype(np.float64) + f64h  # host inputs of the later C3 steps (values only feed timing)
+            ch = np.clip(sh, -1.0, 1.0)
+            return i64h, f64h, sh, ch, ch.astype(np.float32)
+        return get("c3", mk)
+
+    def xh():
+        return get("x", lambda: np.random.default_rng(0).standard_normal((8192, 8192), dtype=np.float32))
+
+    def zh():
+        def mk():
+            r = np.random.default_rng(0)
+            return (r.standard_normal((16, 1024, 1024), dtype=np.float32)
+                    + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
+        return get("z", mk)
+
+    def up(h):
+        return _copies(ms, h, K)
+
+    def row(fn, nbytes, cpu=None):
+        if fn is None:
+            return None, nbytes, cpu
+        # keep the last K results alive, so consecutive launches write K + 1 different output
+        # blocks instead of the one the memory pool would hand back (whose lines the Infinity
+        # Cache still holds)
+        ring = [None] * K
+
+        def g(i):
+            ring[i % K] = fn(i)
+        return g, nbytes, cpu
+
+    def b_add64():
+        A, B = up(a64()), up(b64())
+        return row(lambda i: ms.add(A[i % K], B[i % K]), 12 * 67_108_864,
+                   leg(lambda: R.binary("add", a64(), b64()), 12 * 67_108_864))
+
+    def b_sum64():
+        A = up(a64())
+        return row(lambda i: ms.sum(A[i % K]), 4 * 67_108_864 + 4, leg(lambda: R.reduce(a64(), "sum"), 4 * 67_108_864 + 4))
+
+    def b_argmax64():
+        A = up(a64())
+        return row(lambda i: ms.argmax(A[i % K]), 4 * 67_108_864 + 8,
+                   leg(lambda: R.reduce(a64(), "argmax"), 4 * 67_108_864 + 8))
+
+    def b_sum256():
+        A = up(a256())
+        return row(lambda i: ms.sum(A[i % K]), 4 * 268_435_456 + 4,
+                   leg(lambda: R.reduce(a256(), "sum"), 4 * 268_435_456 + 4))
+
+    def b_argmax256():
+        A = up(a256())
+        return row(lambda i: ms.argmax(A[i % K]), 4 * 268_435_456 + 8,
+                   leg(lambda: R.reduce(a256(), "argmax"), 4 * 268_435_456 + 8))
+
+    def b_bcast():
+        ca, cb = c2()
+        CA, CB = up(ca), up(cb)
+        nb = 4 * 33_554_432 + 4 * 4096 + 4 * 8192
+        return row(lambda i: ms.add(CA[i % K], CB[i % K]), nb, leg(lambda: R.binary("add", ca, cb), nb))
+
+    def b_expT():
+        h = get("xe", lambda: np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32))
+        xt = [ms.transpose(c) for c in up(h)]
+        return row(lambda i: ms.exp(xt[i % K]), 8 * 33_554_432, leg(lambda: R.unary("exp", h.T), 8 * 33_554_432))
+
+    def b_c3add():
+        i64h, f64h, _, _, _ = c3()
+        I, F = up(i64h), up(f64h)
+        return row(lambda i: ms.add(I[i % K], F[i % K]), 24 * N, leg(lambda: R.binary("add", i64h, f64h), 24 * N))
+
+    def c3_dev(stage):
+        i64h, f64h, _, _, _ = c3()
+        I, F = up(i64h), up(f64h)
+        s_ = [ms.add(I[k], F[k]) for k in range(K)]
+        if stage == "s":
+            return s_
+        c_ = [ms.clamp(s_[k], -1.0, 1.0) for k in range(K)]
+        if stage == "c":
+            return c_
+        return [ms.astype(c_[k], "f32") for k in range(K)]
+
+    def b_clamp():
+        s_ = c3_dev("s")
+        sh = c3()[2]
+        return row(lambda i: ms.clamp(s_[i % K], -1.0, 1.0), 16 * N, leg(lambda: R.clamp(sh, -1.0, 1.0), 16 * N))
+
+    def b_f64f32():
+        c_ = c3_dev("c")
+        ch = c3()[3]
+        return row(lambda i: ms.astype(c_[i % K], "f32"), 12 * N, leg(lambda: R.cast(ch, "f32"), 12 * N))
+
+    def b_bf16():
+        f_ = c3_dev("f")
+        fh = c3()[4]
+        return row(lambda i: ms.astype(f_[i % K], "bf16"), 6 * N, leg(lambda: R.cast(fh, "bf16"), 6 * N))
+
+    def b_f16():
+        f_ = c3_dev("f")
+        fh = c3()[4]
+        return row(lambda i: ms.astype(f_[i % K], "f16"), 6 * N, leg(lambda: R.cast(fh, "f16"), 6 * N))
+
+    def b_c4(kind, axis, nbytes):
+        def b():
+            X = up(xh())
+            return row(lambda i: getattr(ms, kind)(X[i % K], axis=axis), nbytes,
+                       leg(lambda: R.reduce(xh(), kind, axis), nbytes))
+        return b
+
+    def b_cumsum():
+        yh = get("y", lambda: np.random.default_rng(0).random((1024, 65536)))
+        Y = up(yh)
+        return row(lambda i: ms.cumsum(Y[i % K], axis=1), 16 * 1024 * 65536,
+                   leg(lambda: R.cumsum(yh, axis=1), 16 * 1024 * 65536))
+
+    def b_cumsum_literal():
         # musapy's literal CPU cumsum re-sums the prefix for every output (O(L^2) per row); rows
         # are independent and cost the same, so one row's rate is the whole array's
-        ops.append(("C5 cumsum f64, literal O(L^2) CPU form (1 of 1024 rows)", None, 16 * 65536,
-                    leg(lambda: R.cumsum(yh[:1], axis=1, literal=True), 16 * 65536)))
-    r = np.random.default_rng(0)
-    z = (r.standard_normal((16, 1024, 1024), dtype=np.float32)
-         + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
-    Z = _copies(ms, z, K)
-    ops.append(("C5 c64 sum axis=(1,2)", lambda i: ms.sum(Z[i % K], axis=(1, 2)), 8 * 16 * 1024 * 1024 + 128,
-                leg(lambda: R.reduce(z, "sum", (1, 2)), 8 * 16 * 1024 * 1024 + 128)))
-    # widened rows: comparisons (1-byte bool output) and complex elementwise
-    M = 16 * 1024 * 1024
-    ops.append(("cmp lt f32 64M -> bool", lambda i: ms.lt(A64[i % K], B64[i % K]), 9 * 67_108_864, None))
-    ops.append(("cmp eq f64 16M -> bool", lambda i: ms.eq(s[i % K], c[i % K]), 17 * N, None))
-    Z2 = [ms.neg(Z[(k + 1) % K]) for k in range(K)]
-    ops.append(("cmp eq c64 16M -> bool", lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M, None))
-    ops.append(("c64 mul 16M", lambda i: ms.mul(Z[i % K], Z2[i % K]), 24 * M, None))
-    ops.append(("c64 div 16M", lambda i: ms.div(Z[i % K], Z2[i % K]), 24 * M, None))
-    ops.append(("c64 abs 16M -> f32", lambda i: ms.abs(Z[i % K]), 12 * M, None))
-    ops.append(("astype f32->c64 64M", lambda i: ms.astype(A64[i % K], "c64"), 12 * 67_108_864, None))
-    W = [ms.astype(Z[k], "c128") for k in range(K)]
-    W2 = [ms.astype(Z2[k], "c128") for k in range(K)]
-    ops.append(("c128 mul 16M", lambda i: ms.mul(W[i % K], W2[i % K]), 48 * M, None))
-    ops.append(("c128 div 16M", lambda i: ms.div(W[i % K], W2[i % K]), 48 * M, None))
-    # contiguous() materialisation: 2-D transpose (transpose2d entry point), 3-D permute, flip
-    ops.append(("contiguous X^T f32 (8192,8192)", lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n, None))
-    P = _copies(ms, np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32), K)
-    ops.append(("contiguous permute(2,0,1) f32 (8192,128,64)",
-                lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n, None))
-    ops.append(("contiguous flip axis=1 f32 (8192,8192)", lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n,
-                None))
-    wm = (r.standard_normal((4096, 4096)) + 1j * r.standard_normal((4096, 4096))).astype(np.complex128)
-    WM = _copies(ms, wm, K)
-    ops.append(("contiguous ^T c128 (4096,4096)", lambda i: ms.contiguous(ms.transpose(WM[i % K])),
-                32 * 4096 * 4096, None))
-    return ops
+        yh = get("y", lambda: np.random.default_rng(0).random((1024, 65536)))
+        return row(None, 16 * 65536, leg(lambda: R.cumsum(yh[:1], axis=1, literal=True), 16 * 65536))
+
+    def b_csum():
+        Z = up(zh())
+        nb = 8 * 16 * 1024 * 1024 + 128
+        return row(lambda i: ms.sum(Z[i % K], axis=(1, 2)), nb, leg(lambda: R.reduce(zh(), "sum", (1, 2)), nb))
+
+    def b_lt():
+        A, B = up(a64()), up(b64())
+        return row(lambda i: ms.lt(A[i % K], B[i % K]), 9 * 67_108_864)
+
+    def b_eqf64():
+        s_, c_ = c3_dev("s"), c3_dev("c")
+        return row(lambda i: ms.eq(s_[i % K], c_[i % K]), 17 * N)
+
+    def zpair():
+        Z = up(zh())
+        return Z, [ms.neg(Z[(k + 1) % K]) for k in range(K)]
+
+    def b_eqc64():
+        Z, Z2 = zpair()
+        return row(lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M)
+
+    def b_cmul(op, dt):
+        def b():
+            Z, Z2 = zpair()
+            if dt == "c128":
+                Z, Z2 = [ms.astype(z, "c128") for z in Z], [ms.astype(z, "c128") for z in Z2]
+            return row(lambda i: getattr(ms, op)(Z[i % K], Z2[i % K]), (48 if dt == "c128" else 24) * M)
+        return b
+
+    def b_cabs():
+        Z = up(zh())
+        return row(lambda i: ms.abs(Z[i % K]), 12 * M)
+
+    def b_f32c64():
+        A = up(a64())
+        return row(lambda i: ms.astype(A[i % K], "c64"), 12 * 67_108_864)
+
+    def b_xT():
+        X = up(xh())
+        return row(lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n)
+
+    def b_perm():
+        P = up(np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32))
+        return row(lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n)
+
+    def b_flip():
+        X = up(xh())
+        return row(lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n)
+
+    def b_c128T():
+        r = np.random.default_rng(2)
+        wm = (r.standard_normal((4096, 4096)) + 1j * r.standard_normal((4096, 4096))).astype(np.complex128)
+        WM = up(wm)
+        return row(lambda i: ms.contiguous(ms.transpose(WM[i % K])), 32 * 4096 * 4096)
+
+    return [
+        ("add64", "C1-64M add f32 67,108,864", b_add64),
+        ("sum64", "full sum f32 64M", b_sum64),
+        ("argmax64", "full argmax f32 64M", b_argmax64),
+        ("sum256", "full sum f32 256M", b_sum256),
+        ("argmax256", "full argmax f32 256M", b_argmax256),
+        ("bcast", "C2 broadcast add (4096,1)+(8192,)", b_bcast),
+        ("expT", "C2 exp transposed (8192,4096)^T", b_expT),
+        ("c3add", "C3 add i64+f64->f64 (fused promotion)", b_c3add),
+        ("clamp", "C3 clamp f64", b_clamp),
+        ("f64f32", "C3 astype f64->f32", b_f64f32),
+        ("bf16", "C3 astype f32->bf16", b_bf16),
+        ("f16", "C3 astype f32->f16", b_f16),
+        ("sum0", "C4 sum axis=0", b_c4("sum", 0, 4 * n + 4 * 8192)),
+        ("mean1", "C4 mean axis=-1", b_c4("mean", -1, 4 * n + 4 * 8192)),
+        ("mean0", "C4 mean axis=0", b_c4("mean", 0, 4 * n + 4 * 8192)),
+        ("max01", "C4 max axis=(0,1)", b_c4("max", (0, 1), 4 * n + 4)),
+        ("argmin1", "C4 argmin axis=1", b_c4("argmin", 1, 4 * n + 8 * 8192)),
+        ("cumsum", "C5 cumsum f64 (1024,65536) axis=1", b_cumsum),
+        ("cumsum_literal", "C5 cumsum f64, literal O(L^2) CPU form (1 of 1024 rows)", b_cumsum_literal),
+        ("csum", "C5 c64 sum axis=(1,2)", b_csum),
+        ("lt", "cmp lt f32 64M -> bool", b_lt),
+        ("eqf64", "cmp eq f64 16M -> bool", b_eqf64),
+        ("eqc64", "cmp eq c64 16M -> bool", b_eqc64),
+        ("c64mul", "c64 mul 16M", b_cmul("mul", "c64")),
+        ("c64div", "c64 div 16M", b_cmul("div", "c64")),
+        ("c64abs", "c64 abs 16M -> f32", b_cabs),
+        ("f32c64", "astype f32->c64 64M", b_f32c64),
+        ("c128mul", "c128 mul 16M", b_cmul("mul", "c128")),
+        ("c128div", "c128 div 16M", b_cmul("div", "c128")),
+        ("xT", "contiguous X^T f32 (8192,8192)", b_xT),
+        ("permute", "contiguous permute(2,0,1) f32 (8192,128,64)", b_perm),
+        ("flip", "contiguous flip axis=1 f32 (8192,8192)", b_flip),
+        ("c128T", "contiguous ^T c128 (4096,4096)", b_c128T),
+    ]
 
 
 def interop_costs(ms):
@@ -291,6 +444,44 @@ def cpu_baseline(host):
     return algo * reps / el / 1e9, el / reps, f"the full step (C1 add 16M + C4 sum axis=-1 + C4 argmax axis=1), {reps} passes"
 
 
+def mall_flushed(ms, ops, timer, steps):
+    """Each op launched `steps` times, every launch timed alone by HIP events right after 768 MB of
+    other traffic (an add over three 256 MB buffers) has replaced what the 256 MB Infinity Cache
+    held: a cold-cache figure beside the back-to-back one.  Returns {name: average ms}."""
+    h = np.full(67_108_864, 1.0, np.float32)
+    F = [ms.from_numpy(h) for _ in range(3)]
+    del h
+    per = {}
+    for _, name, fn, _ in ops:
+        tot = 0.0
+        for i in range(steps):
+            ms.add(F[0], F[1], out=F[2])
+            tot += timer.run([lambda i=i, fn=fn: fn(i)])
+        per[name] = tot / steps
+    return per
+
+
+def run_only(ms, key, warmup, steps):
+    """--only KEY: launch one op warmup+steps times (the program rocprofv3 --pmc profiles)."""
+    if key in ("add", "sum", "argmax", "copy"):
+        ops, _ = step_ops(ms)
+        key, name, fn, bytes_ = next(o for o in ops if o[0] == key)
+    else:
+        rows = {k: (n, b) for k, n, b in all_config_ops(ms)}
+        if key not in rows:
+            print(f"unknown --only key {key!r}; config keys: {', '.join(rows)}", file=sys.stderr)
+            sys.exit(2)
+        name, build = rows[key]
+        fn, bytes_, _ = build()
+        if fn is None:
+            print(f"--only {key}: a CPU-only row", file=sys.stderr)
+            sys.exit(2)
+    for i in range(warmup + steps):
+        fn(i)
+    ms.synchronize()
+    print(json.dumps({"only": key, "op": name, "launches": warmup + steps, "algo_bytes": bytes_}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -301,15 +492,10 @@ def main():
     import musapy_amd as ms
 
     timer = Timer(ms)
-    ops, host = step_ops(ms)
     if args.only:
-        key, name, fn, bytes_ = next(o for o in ops if o[0] == args.only)
-        for i in range(args.warmup + args.steps):
-            fn(i)
-        ms.synchronize()
-        print(json.dumps({"only": key, "op": name, "launches": args.warmup + args.steps, "algo_bytes": bytes_}),
-              flush=True)
+        run_only(ms, args.only, args.warmup, args.steps)
         return
+    ops, host = step_ops(ms)
     ops = [o for o in ops if o[0] != "copy"]
     for _, name, fn, _ in ops:  # warm-up (first launches load code objects, fill the memory pool)
         for i in range(max(args.warmup, 1)):
@@ -318,8 +504,8 @@ def main():
     per_op = {}
     t0 = time.perf_counter()
     ms.synchronize()
-    # K steps: each op is launched K times back-to-back between two events (inputs rotate over
-    # COPIES device copies, so every launch streams from HBM)
+    # K steps: each op is launched K times back-to-back between two events (inputs and outputs
+    # rotate over COPIES device buffers, so every launch streams from HBM)
     for _, name, fn, _ in ops:
         per_op[name] = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(args.steps)])
     ms.synchronize()
@@ -337,6 +523,8 @@ def main():
     dom = max(table, key=lambda k: table[k]["ms"])
     traffic = measured_traffic().get(keys[dom])
     value = total_bytes / total_ms / 1e6
+    cold = mall_flushed(ms, ops, timer, args.steps)
+    cold_ms = sum(cold.values())
     line = {
         "metric": "achieved HBM GB/s (and % of MI355X peak) for f32 add, axis-sum, argmax",
         "value": round(value, 1),
@@ -346,7 +534,8 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(total_ms, 5),
         "wall_ms_per_step": round(wall * 1e3 / args.steps, 3),
-        "timing": f"HIP events around {args.steps} back-to-back launches per op, inputs rotated over {COPIES} copies",
+        "timing": f"HIP events around {args.steps} back-to-back launches per op, inputs and outputs rotated over "
+                  f"{COPIES} buffers",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -356,6 +545,10 @@ def main():
                    "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "ops": table,
+        "mall_flushed": {"value": round(total_bytes / cold_ms / 1e6, 1), "ms_per_step": round(cold_ms, 5),
+                         "ops_ms": {k: round(v, 5) for k, v in cold.items()},
+                         "method": "each launch timed alone by HIP events after 768 MB of other traffic "
+                                   "(add over three 256 MB buffers) flushed the Infinity Cache"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["GBps"], "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": traffic,
                      "algo_bytes": table[dom]["algo_bytes"],
@@ -367,11 +560,15 @@ def main():
         line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                                 "sample": sample, "seconds_per_pass": round(sec, 3), "host": host_cpu()}
     if args.all:
+        del ops, host
         rows = []
-        for name, fn, bytes_, cpu in all_config_ops(ms, host_legs=not args.no_cpu):
-            row = {"op": name}
+        for key, name, build in all_config_ops(ms, host_legs=not args.no_cpu):
+            gc.collect()  # free the previous row's device arrays before this row is timed
+            fn, bytes_, cpu = build()
+            row = {"op": name, "key": key}
             if fn is not None:
-                fn(0)
+                for i in range(8):  # fill the output ring and the memory pool before timing
+                    fn(i)
                 ms.synchronize()
                 t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(20)])
                 row.update({"ms": round(t, 5), "GBps": round(bytes_ / t / 1e6, 1),
@@ -381,6 +578,7 @@ def main():
                 covered = cpu()
                 row["cpu_GBps"] = round(covered / (time.perf_counter() - t0) / 1e9, 3)
             rows.append(row)
+            del fn, cpu
             print(json.dumps(row), file=sys.stderr, flush=True)
         line["all_configs"] = rows
         line["interop"] = interop_costs(ms)

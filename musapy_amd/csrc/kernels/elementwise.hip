@@ -39,7 +39,7 @@ struct In {
 // flat: 1-D, every input contiguous (mode 1) or scalar (mode 0).  Full tiles use VEC-wide
 // vector accesses; the final partial tile falls back to one element per lane.
 template <int VEC, int UNROLL, class F, class TO, class TA>
-__global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict__ c, uint64_t n, F f) {
+__global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict__ c, uint64_t n, bool nts, F f) {
   constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
   const uint64_t base = uint64_t(blockIdx.x) * kTile;
   const int t = threadIdx.x;
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict_
       Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k]);
-      vstore_out<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+      vstore_pol<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc, nts);
     }
   } else {
     for (uint64_t i = base + t; i < n; i += kBlock) c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i]);
@@ -69,7 +69,8 @@ __global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict_
 
 // TO: the output element type (T for arithmetic, uint8_t for comparisons)
 template <int VEC, int UNROLL, class F, class T, class TO = T>
-__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __restrict__ c, uint64_t n, F f) {
+__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __restrict__ c, uint64_t n, bool nts,
+                                                        F f) {
   constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
   const uint64_t base = uint64_t(blockIdx.x) * kTile;
   const int t = threadIdx.x;
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __
       Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k], vb[u].v[k]);
-      vstore_out<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc);
+      vstore_pol<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc, nts);
     }
   } else {
     for (uint64_t i = base + t; i < n; i += kBlock)
@@ -138,7 +139,8 @@ __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t co
 
 template <int VEC, int UNROLL, class F, class TO, class TA>
 __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO* __restrict__ c, RowIndexer<2> ix,
-                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, F f) {
+                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, bool nts,
+                                                       F f) {
   const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k]);
-      vstore_out<TO, VEC>(cp, v);
+      vstore_pol<TO, VEC>(cp, v, nts);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
 template <int VEC, int UNROLL, class F, class T, class TO = T>
 __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<T> b, int64_t sb, TO* __restrict__ c,
                                                         RowIndexer<3> ix, FastDiv gpr, uint32_t L, uint32_t items,
-                                                        bool aligned, F f) {
+                                                        bool aligned, bool nts, F f) {
   const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k], y[k]);
-      vstore_out<TO, VEC>(cp, v);
+      vstore_pol<TO, VEC>(cp, v, nts);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
 // reference's cast-then-compute (op_builder.rs:410-417) without materialising the cast.
 template <int VEC, class F, class TC, class TA, class TB>
 __global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restrict__ a, const TB* __restrict__ b,
-                                                              TC* __restrict__ c, uint64_t n, bool nt, F f) {
+                                                              TC* __restrict__ c, uint64_t n, bool nt, bool nts, F f) {
   const uint64_t i0 = (uint64_t(blockIdx.x) * kBlock + threadIdx.x) * VEC;
   const CastF<TA, TC> ca{};
   const CastF<TB, TC> cb{};
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restri
     Vec<TC, VEC> z;
 #pragma unroll
     for (int k = 0; k < VEC; ++k) z.v[k] = f(ca(x.v[k]), cb(y.v[k]));
-    vstore_out<TC, VEC>(c + i0, z);
+    vstore_pol<TC, VEC>(c + i0, z, nts);
   } else {
     for (uint64_t i = i0; i < n; ++i) c[i] = f(ca(a[i]), cb(b[i]));
   }
@@ -230,6 +232,7 @@ struct RowPieceArgs {
   uint32_t L;         // row length (innermost output dim)
   FastDiv groups;     // blocks per row
   bool aligned;       // every item full and 16-byte aligned (host-checked)
+  bool nts;           // streaming stores
 };
 
 template <int VEC, int U, class F, class T, class TO = T>
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(xa[u][k], xb[u][k]);
-      vstore_out<TO, VEC>(cp, v);
+      vstore_pol<TO, VEC>(cp, v, ra.nts);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -277,6 +280,7 @@ struct TransposeArgs {
   RowIndexer<2> batch;     // batch dims: [0] output strides, [1] input strides
   bool vec_in, vec_out;    // 16-byte aligned vector access possible on each side
   bool nt;                 // streaming loads
+  bool nts;                // streaming stores
 };
 
 // Tile geometry: PL lanes x VI elements along P (input-contiguous) by TL along L
@@ -353,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
         Vec<TO, VO> v;
 #pragma unroll
         for (int q = 0; q < VO; ++q) v.v[q] = tile[ll + q][pp];
-        vstore_out<TO, VO>(dst, v);
+        vstore_pol<TO, VO>(dst, v, ta.nts);
       } else {
 #pragma unroll
         for (int q = 0; q < VO; ++q)
@@ -529,15 +533,16 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
   // the narrower type moves 16 bytes per item, the wider one 16-32 (e.g. f64->f32: 4 elements)
   constexpr int V = ew_vec<TA, TO>();
   const bool nt = operand_elems(p, 1) * sizeof(TA) >= kStreamLoadBytes;
+  const bool nts = p.numel * sizeof(TO) >= kStreamStoreBytes;
   if (p.ndim == 1 && p.stride[0][0] == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1)) {
     In<TA> ia{a, mode_of(p.stride[1][0]), nt};
     bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a));
     if (vec_ok) {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
-      k_unary_flat<V, kFlatUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
+      k_unary_flat<V, kFlatUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, nts, f);
     } else {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
-      k_unary_flat<1, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, f);
+      k_unary_flat<1, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, nts, f);
     }
     return;
   }
@@ -561,6 +566,7 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
         ta.vec_in = aligned16(a) && (uint64_t(sL < 0 ? -sL : sL) * sizeof(TA)) % 16 == 0;
         ta.vec_out = aligned16(c) && (uint64_t(ta.out_sP) * sizeof(TO)) % 16 == 0;
         ta.nt = true;  // tiles read across many rows at once: streaming won at 128 MB too (5.1 vs 4.9 TB/s)
+        ta.nts = nts;
         for (int d = nd - 2; d >= 0; --d) {
           if (d == P) continue;
           int k = ta.batch.nd++;
@@ -582,7 +588,8 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<2> ix = make_row_indexer<2>(p);
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-    k_unary_rows<V, kUnroll, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items, al, f);
+    k_unary_rows<V, kUnroll, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items, al, nts,
+                                                                 f);
     return;
   }
   k_unary_generic<F, TO, TA><<<grid_generic(p.numel), kBlock, 0, st>>>(a, c, make_meta64(p), p.numel, f);
@@ -597,6 +604,7 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
   constexpr int V = vec_of<T>();
   const int nd = p.ndim;
   const bool nt = (operand_elems(p, 1) + operand_elems(p, 2)) * sizeof(T) >= kStreamLoadBytes;
+  const bool nts = p.numel * sizeof(TO) >= kStreamStoreBytes;
   if (nd == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1) && (p.stride[2][0] == 0 || p.stride[2][0] == 1)) {
     In<T> ia{a, mode_of(p.stride[1][0]), nt}, ib{b, mode_of(p.stride[2][0]), nt};
     constexpr uintptr_t kOutAlign = sizeof(TO) * V < 16 ? sizeof(TO) * V : 16;  // one output vector
@@ -604,10 +612,10 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
                   (ib.mode == kModeScalar || aligned16(b));
     if (vec_ok) {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
-      k_binary_flat<V, kFlatUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+      k_binary_flat<V, kFlatUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, nts, f);
     } else {
       uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
-      k_binary_flat<1, kUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, f);
+      k_binary_flat<1, kUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, nts, f);
     }
     return;
   }
@@ -626,6 +634,7 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
       ra.ix = ix;
       ra.L = L;
       ra.aligned = al;
+      ra.nts = nts;
       const uint32_t groups = (L + uint32_t(kBlock) * V * U - 1) / (uint32_t(kBlock) * V * U);
       ra.groups = make_fastdiv(groups);
       const uint64_t blocks = uint64_t(p.numel / L) * groups;
@@ -636,7 +645,7 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
     }
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
     k_binary_rows<V, kUnroll, F, T, TO><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al,
-                                                                 f);
+                                                                 nts, f);
     return;
   }
   k_binary_generic<F, T, TO><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
@@ -656,7 +665,8 @@ void launch_binary_mixed(const void* a, const void* b, void* c, int ndim, const 
   if (p.ndim == 1 && p.stride[1][0] == 1 && p.stride[2][0] == 1 && aligned16(a) && aligned16(b) && aligned16(c)) {
     const uint64_t blocks = (p.numel + uint64_t(kBlock) * V - 1) / (uint64_t(kBlock) * V);
     const bool nt = p.numel * (sizeof(TA) + sizeof(TB)) >= kStreamLoadBytes;
-    k_binary_flat_mixed<V, F, TC, TA, TB><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(pa, pb, pc, p.numel, nt, f);
+    const bool nts = p.numel * sizeof(TC) >= kStreamStoreBytes;
+    k_binary_flat_mixed<V, F, TC, TA, TB><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(pa, pb, pc, p.numel, nt, nts, f);
     return;
   }
   k_binary_generic_mixed<F, TC, TA, TB><<<grid_generic(p.numel), kBlock, 0, st>>>(pa, pb, pc, make_meta64(p),

@@ -115,24 +115,29 @@ __device__ inline void vstore_nt(T* p, const Vec<T, N>& v) {
 }
 
 // Load policy of the elementwise kernels by volume: a launch that streams at least this many
-// input bytes uses streaming loads; below it, default loads.  Measured on MI355X: at 256 MB of
-// input streaming loads win by 10-15% (64M add 7.0 vs 5.9 TB/s), at 128 MB default loads win by
-// 4-10% (16M add 6.6 vs 6.35, f32->bf16 6.1 vs 5.4) -- the 256 MB Infinity Cache sits between
-// the two.  Reductions always stream (they write next to nothing).
-constexpr uint64_t kStreamLoadBytes = uint64_t(192) << 20;
+// input bytes uses streaming loads; below it, default loads (small inputs are often read again
+// and are worth keeping in the caches).  Measured on MI355X with outputs rotated over 4 buffers,
+// so that each launch's writes reach HBM: 16M f32 add (128 MB of input) 31.7-32.0 us with
+// streaming loads against 35.7-36.2 with default loads, C3's i64 + f64 75 vs 82 us, f64 -> f32
+// 33.8 vs 35.2 us.  (Writing the same output buffer every launch, the Infinity Cache absorbs the
+// writes and favours default loads below 192 MB; that is not what a pipeline of ops sees.)
+// Reductions always stream (they write next to nothing).
+constexpr uint64_t kStreamLoadBytes = uint64_t(32) << 20;
 
 template <typename T, int N>
 __device__ inline Vec<T, N> vload_pol(const T* p, bool nt) {
   return nt ? vload_nt<T, N>(p) : vload<T, N>(p);
 }
 
-// Stores of a launch's output.  Outputs come from the memory pool, which hands the same
-// addresses back op after op, so the Infinity Cache absorbs and merges their writes; streaming
-// stores measured slower on that pattern (16M f32 add 6.1 vs 6.4 TB/s) and are kept off.
-constexpr bool kStreamStores = false;
+// Store policy of the elementwise kernels by volume: an output of at least this many bytes is
+// written with streaming stores.  Such an output does not stay in the 256 MB Infinity Cache for
+// its consumer anyway; measured on MI355X with outputs rotated over 4 buffers, streaming stores
+// moved the (8192, 8192) f32 transpose 112.5 -> 107 us, a flip 98 -> 91 us, the c128 transpose
+// 111 -> 102 us and c128 mul/div 130 -> 124 us, and left the other configs unchanged.
+constexpr uint64_t kStreamStoreBytes = uint64_t(64) << 20;
 template <typename T, int N>
-__device__ inline void vstore_out(T* p, const Vec<T, N>& v) {
-  if constexpr (kStreamStores) vstore_nt<T, N>(p, v); else vstore<T, N>(p, v);
+__device__ inline void vstore_pol(T* p, const Vec<T, N>& v, bool nt) {
+  if (nt) vstore_nt<T, N>(p, v); else vstore<T, N>(p, v);
 }
 
 // ---------------------------------------------------------------------------------------------
