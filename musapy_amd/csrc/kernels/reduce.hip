@@ -483,6 +483,121 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
 }
 
 // --------------------------------------------------------------------------------------------
+// max / min over both axes of a C-contiguous (R, C) array in one launch, with the result the
+// reference's two passes give (reduce_multi, reduction.rs:118-155: axis 0 with keepdims, then
+// axis 1).  Pass 1 keeps, per column, the first row holding the column's extreme, and a column
+// whose row-0 element is NaN becomes NaN; pass 2 keeps the first column holding the extreme of
+// those columns and skips NaN ones, unless column 0 is NaN, which absorbs everything.  So the
+// result is the element of extreme value that comes first in COLUMN-major order, among the
+// non-NaN elements of the columns whose row 0 is not NaN -- or x[0][0] when that is NaN.  This
+// kernel computes exactly that: a persistent grid walks whole rows (block b takes rows b, b+G,
+// ...; lane l owns columns (k * 512 + l) * V .. + V - 1, k < KC), keeping one (value, row)
+// accumulator per owned column; then each lane folds its columns with the column-major index
+// col * R + row as the tie-break, skipping columns whose row-0 element is NaN, the blocks
+// publish, and the combiner block (index G) folds the G results in a fixed order.
+template <class Op, class OpF, class T, int KC>
+__global__ __launch_bounds__(kRowBS) void k_reduce_2d_ordered(const T* __restrict__ a, uint64_t R, uint64_t C,
+                                                              uint32_t grid, RedOut<T> out, FusedArgs fa) {
+  using A = typename Op::A;    // (value, row) per column, rows < 2^31
+  using AF = typename OpF::A;  // (value, column-major index)
+  static_assert(sizeof(AF) % 4 == 0, "accumulator must split into 32-bit slices");
+  constexpr int W = int(sizeof(AF) / 4);
+  constexpr int V = int(16 / sizeof(T));
+  const uint32_t b = blockIdx.x;
+  if (b < grid) {
+    A acc[KC][V];
+#pragma unroll
+    for (int k = 0; k < KC; ++k)
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[k][v] = Op::init();
+    bool own[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) own[k] = (uint64_t(k) * kRowBS + threadIdx.x) * V < C;  // C % V == 0
+    // rows of this block, software pipelined: the next row's loads are in flight while the
+    // current one is folded (rows arrive in increasing order, so Op::step keeps the first)
+    Vec<T, V> x[KC], y[KC];
+    auto load = [&](uint64_t r, Vec<T, V>(&dst)[KC]) {
+      const T* row = a + r * C;
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+        if (own[k]) dst[k] = vload_nt<T, V>(row + (uint64_t(k) * kRowBS + threadIdx.x) * V);
+    };
+    auto fold = [&](uint64_t r, const Vec<T, V>(&src)[KC]) {
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+        if (own[k])
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[k][v] = Op::step(acc[k][v], src[k].v[v], int64_t(r));
+    };
+    uint64_t r = b;
+    if (r < R) {
+      load(r, x);
+      for (;;) {
+        const uint64_t r1 = r + grid;
+        if (r1 >= R) {
+          fold(r, x);
+          break;
+        }
+        load(r1, y);
+        fold(r, x);
+        const uint64_t r2 = r1 + grid;
+        if (r2 >= R) {
+          fold(r1, y);
+          break;
+        }
+        load(r2, x);
+        fold(r1, y);
+        r = r2;
+      }
+    }
+    // the lane's columns -> one key; a column whose row-0 element is NaN is skipped (pass 2)
+    AF best = OpF::init();
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      if (!own[k]) continue;
+      const uint64_t c0 = (uint64_t(k) * kRowBS + threadIdx.x) * V;
+      const Vec<T, V> top = vload<T, V>(a + c0);  // row 0, shared by every block (cache hits)
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        if (acc[k][v].idx >= 0 && !is_nan(top.v[v]))
+          best = OpF::comb(best, AF{acc[k][v].val, int64_t(c0 + v) * int64_t(R) + int64_t(acc[k][v].idx)});
+    }
+    best = group_reduce<OpF, kRowBS>(best, R * C < 0xffffffffull);
+    if (threadIdx.x == 0) {
+      uint32_t s[W];
+      __builtin_memcpy(s, &best, sizeof(AF));
+      publish_slices<W>(fa.slots + uint64_t(b) * W, s);
+    }
+    return;
+  }
+  // combiner: lane l folds block results l, l + 512 (PER = 2 at most), then the block tree
+  constexpr int PER = 2;
+  uint64_t vv[PER][W];
+  const bool ok = gather_published<W, PER>(fa.slots, grid, fa.spin_limit, vv);
+  AF res = OpF::init();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t bb = threadIdx.x + j * kRowBS;
+    if (bb >= grid) break;
+    uint32_t s[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) s[i] = uint32_t(vv[j][i]);
+    AF xv;
+    __builtin_memcpy(&xv, s, sizeof(AF));
+    res = OpF::comb(res, xv);
+#pragma unroll
+    for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
+  }
+  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
+  res = group_reduce<OpF, kRowBS>(res, R * C < 0xffffffffull);
+  if (threadIdx.x == 0) {
+    const T x00 = a[0];
+    if (is_nan(x00)) res = AF{x00, 0};  // column 0 is NaN: it absorbs the second pass
+    write_result<OpF, T, kWriteFinal>(out, 0, res, 0);
+  }
+}
+
+// --------------------------------------------------------------------------------------------
 // col kernel: block = (outer, column group, tile); 64 lanes x VEC columns, 4 waves split rows.
 struct ColArgs {
   RowIndexer<1> ix;   // outer output dims (all but the innermost one) -> input offset
@@ -923,6 +1038,32 @@ int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid
   return kFusedLaunched;
 }
 
+
+// max / min over both axes of a C-contiguous, 16-byte aligned (R, C) array in one launch
+// (k_reduce_2d_ordered); kFusedNotCovered when the shape does not fit it
+template <class Op, class OpF, class T>
+int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, void* ws, size_t ws_bytes,
+                             hipStream_t st) {
+  constexpr int V = rvec<T>();
+  if (R == 0 || C == 0 || ws == nullptr || !al16(a) || C % V || R >= (uint64_t(1) << 31)) return kFusedNotCovered;
+  const uint64_t kc = ceil_div(C, uint64_t(kRowBS) * V);
+  if (kc > 4 || R * C >= (uint64_t(1) << 62)) return kFusedNotCovered;
+  const uint32_t grid = uint32_t(R < 2 * kRowBS ? R : 2 * kRowBS);  // the combiner folds up to 2 * 512 slots
+  const uint64_t W = sizeof(typename OpF::A) / 4;
+  if (uint64_t(grid) * W * 8 > ws_bytes) return kFusedNoRoom;
+  FusedArgs fa{};
+  fa.slots = static_cast<uint64_t*>(ws);
+  fa.fault = device_fault_word(st);
+  fa.spin_limit = wait_spin_limit();
+  if (fa.fault == nullptr) return kFusedNotCovered;
+  const dim3 g(grid + 1);
+  switch (kc) {
+    case 1: k_reduce_2d_ordered<Op, OpF, T, 1><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
+    case 2: k_reduce_2d_ordered<Op, OpF, T, 2><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
+    default: k_reduce_2d_ordered<Op, OpF, T, 4><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
+  }
+  return kFusedLaunched;
+}
 }  // namespace mpy
 
 
@@ -1174,6 +1315,31 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
                            const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles,
                            void* workspace, size_t workspace_bytes, hipStream_t st) {
   const int r = fused_dispatch(op, dtype, a, c, RED_PASS, tiles, workspace, workspace_bytes, st);
+  return r == kFusedLaunched ? 0 : -1;
+}
+
+// max / min over both axes of a C-contiguous (rows, cols) array in one launch, with the result of
+// the reference's two per-axis passes (new; see musapy_kernels.h)
+int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_t rows, size_t cols,
+                                void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (op != MUSAPY_RED_MAX && op != MUSAPY_RED_MIN) return -1;
+  const bool mx = op == MUSAPY_RED_MAX;
+  int r = kFusedNotCovered;
+#define RED2D(T)                                                                                                \
+  {                                                                                                             \
+    const T* x = static_cast<const T*>(a);                                                                      \
+    RedOut<T> o = vout<T>(static_cast<T*>(c));                                                                  \
+    r = mx ? launch_reduce_2d_ordered<OpExt<T, true, false>, OpExt<T, true, false, int64_t>, T>(                \
+                 x, o, rows, cols, workspace, workspace_bytes, st)                                              \
+           : launch_reduce_2d_ordered<OpExt<T, false, false>, OpExt<T, false, false, int64_t>, T>(              \
+                 x, o, rows, cols, workspace, workspace_bytes, st);                                             \
+  }
+  switch (dtype) {
+    case MUSAPY_DT_F32: RED2D(float) break;
+    case MUSAPY_DT_F64: RED2D(double) break;
+    case MUSAPY_DT_I64: RED2D(int64_t) break;
+  }
+#undef RED2D
   return r == kFusedLaunched ? 0 : -1;
 }
 

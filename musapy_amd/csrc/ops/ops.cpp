@@ -760,6 +760,28 @@ Array reduce_multi(const Array& a, const std::vector<ssize_t>* axes, bool keepdi
       return cur->view(Layout::from_shape(target));  // results are C-contiguous
     }
   }
+  if ((k == ReduceKernel::Max || k == ReduceKernel::Min) && a.ndim() == 2 && ax.size() == 2 && a.is_contiguous() &&
+      a.size() > 0) {
+    // both axes of a C-contiguous matrix: one launch with the per-axis passes' result
+    int dt = -1;
+    if (a.dtype == Dtype::Float32) dt = MUSAPY_DT_F32;
+    else if (a.dtype == Dtype::Float64) dt = MUSAPY_DT_F64;
+    else if (a.dtype == Dtype::Int64) dt = MUSAPY_DT_I64;
+    if (dt >= 0) {
+      StreamPtr s = pick_stream(a, nullptr);
+      Array r = make_output(nullptr, keepdims ? Shape{1, 1} : Shape{}, a.dtype, a.device, s, {&a});
+      a.data->wait_last_write_on(s);
+      const int op = k == ReduceKernel::Max ? MUSAPY_RED_MAX : MUSAPY_RED_MIN;
+      if (musapy_reduce_2d_ordered_v1(op, dt, a.data_ptr(), r.data_ptr(), a.shape()[0], a.shape()[1],
+                                      s->reduce_workspace(), Stream::kReduceWorkspaceBytes, s->raw()) == 0) {
+        s->note_bounded_wait();
+        check_launch(rname(k));
+        a.data->record_read(s);
+        r.data->record_write(s);
+        return r;
+      }
+    }
+  }
   std::optional<Array> cur;
   for (size_t x : ax) cur = reduction_axis(cur ? *cur : a, x, true, nullptr, k);
   if (keepdims) return *cur;

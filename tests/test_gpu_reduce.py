@@ -407,3 +407,33 @@ def test_cumsum_look_back_long_rows():
                 bound = bound + np.abs(want - exact)
             assert np.all(np.abs(got.astype(np.float64) - want) <= bound), what
         assert_bits_equal(ms.cumsum(X, axis=1).numpy(), got, what + " run-to-run")
+
+
+@pytest.mark.parametrize("kind", ["max", "min"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64])
+def test_two_axis_single_launch(kind, dt):
+    """max/min over (0, 1) of a C-contiguous matrix run as one launch (musapy_reduce_2d_ordered_v1)
+    that must give the per-axis passes' bits: the first extreme in COLUMN-major order.  A zero of
+    one sign that comes first row-major and of the other sign first column-major tells the two
+    orders apart; rows span several blocks of the persistent grid; keepdims keeps (1, 1)."""
+    sign = 1 if kind == "max" else -1
+    for shape in ((8192, 8192), (3000, 2048), (2500, 4096), (5, 8), (1, 12), (1500, 8188)):
+        if dt == np.int64:
+            x = RNG.integers(-10**6, 10**6, shape).astype(np.int64)
+        else:
+            x = RNG.standard_normal(shape).astype(dt)
+        check_reduce(kind, x, (0, 1))
+        check_reduce(kind, x, (0, 1), keepdims=True)
+        if dt == np.int64:
+            continue
+        z = np.full(shape, -sign, dt)
+        z[0, shape[1] - 1] = -0.0          # first extreme in row-major order
+        z[shape[0] - 1, 0 if shape[1] == 1 else 1] = 0.0  # first in column-major order: its bits win
+        check_reduce(kind, z, (0, 1))
+        y = x.copy()
+        y[0, 3] = np.nan                   # drops column 3, whatever it holds below
+        y[shape[0] - 1, 3] = sign * 1e30
+        y[shape[0] // 2, 5] = np.nan       # skipped
+        check_reduce(kind, y, (0, 1))
+        y[0, 0] = np.nan                   # absorbs everything
+        check_reduce(kind, y, (0, 1))
