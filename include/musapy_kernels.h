@@ -325,15 +325,15 @@ enum { MUSAPY_RED_SUM = 0, MUSAPY_RED_PROD, MUSAPY_RED_MAX, MUSAPY_RED_MIN, MUSA
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- max / min over both axes of a 2-D array in one launch (new; no counterpart in kernels.rs) ----
- * `a` is a C-contiguous (rows, cols) array of the compute dtype (F32, F64 or I64), 16-byte
- * aligned, and `c` receives one value.  The result is bit for bit what the reference's per-axis
+ * `a` is a C-contiguous (rows, cols) array of the compute dtype (F32, F64 or I64), and `c`
+ * receives one value.  The result is bit for bit what the reference's per-axis
  * passes give (rust/musapy-ops/src/reduction.rs:118-155: axis 0 with keepdims, then axis 1), NaN
  * and signed-zero outcomes included: the first extreme element in column-major order, among the
  * non-NaN elements of the columns whose row-0 element is not NaN, or a[0][0] when that is NaN.
  * `op` is MUSAPY_RED_MAX or MUSAPY_RED_MIN; `workspace` follows musapy_reduce_fused_v1's rules
  * (zero before the first call, left zero; 1024 slots of 4 words at most).  Returns 0 when
- * launched, -1 when not covered (cols above 8192 f32 / 4096 f64 and i64 elements, cols not a
- * multiple of the 16-byte vector, rows >= 2^31, or a misaligned `a`): then reduce per axis. */
+ * launched, -1 when not covered (more than 1024 groups of 64 16-byte column vectors, or rows >=
+ * 2^31): then reduce per axis. */
 int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_t rows, size_t cols, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- single-launch reduction that allocates nothing (new; no counterpart in kernels.rs) ----

@@ -269,13 +269,13 @@ struct FusedArgs {
 // Gathers the published W-word slots lane, lane + kRowBS, ... (below `count`) into v: all
 // outstanding slots' words are loaded together, the ready ones kept, the rest polled again.
 // Returns false when the poll budget ran out with slots still unpublished.
-template <int W, int PER>
+template <int W, int PER, int STRIDE = kRowBS>
 __device__ inline bool gather_published(const uint64_t* slots, uint32_t count, uint32_t spin_limit,
                                         uint64_t (&v)[PER][W]) {
   uint32_t pending = 0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    if (threadIdx.x + j * kRowBS < count) pending |= 1u << j;
+    if (threadIdx.x + j * STRIDE < count) pending |= 1u << j;
 #pragma unroll
     for (int i = 0; i < W; ++i) v[j][i] = 0;
   }
@@ -284,7 +284,7 @@ __device__ inline bool gather_published(const uint64_t* slots, uint32_t count, u
     for (int j = 0; j < PER; ++j)
       if (pending & (1u << j))
 #pragma unroll
-        for (int i = 0; i < W; ++i) v[j][i] = ld_relaxed(slots + uint64_t(threadIdx.x + j * kRowBS) * W + i);
+        for (int i = 0; i < W; ++i) v[j][i] = ld_relaxed(slots + uint64_t(threadIdx.x + j * STRIDE) * W + i);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       bool ready = true;
@@ -483,121 +483,6 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
 }
 
 // --------------------------------------------------------------------------------------------
-// max / min over both axes of a C-contiguous (R, C) array in one launch, with the result the
-// reference's two passes give (reduce_multi, reduction.rs:118-155: axis 0 with keepdims, then
-// axis 1).  Pass 1 keeps, per column, the first row holding the column's extreme, and a column
-// whose row-0 element is NaN becomes NaN; pass 2 keeps the first column holding the extreme of
-// those columns and skips NaN ones, unless column 0 is NaN, which absorbs everything.  So the
-// result is the element of extreme value that comes first in COLUMN-major order, among the
-// non-NaN elements of the columns whose row 0 is not NaN -- or x[0][0] when that is NaN.  This
-// kernel computes exactly that: a persistent grid walks whole rows (block b takes rows b, b+G,
-// ...; lane l owns columns (k * 512 + l) * V .. + V - 1, k < KC), keeping one (value, row)
-// accumulator per owned column; then each lane folds its columns with the column-major index
-// col * R + row as the tie-break, skipping columns whose row-0 element is NaN, the blocks
-// publish, and the combiner block (index G) folds the G results in a fixed order.
-template <class Op, class OpF, class T, int KC>
-__global__ __launch_bounds__(kRowBS) void k_reduce_2d_ordered(const T* __restrict__ a, uint64_t R, uint64_t C,
-                                                              uint32_t grid, RedOut<T> out, FusedArgs fa) {
-  using A = typename Op::A;    // (value, row) per column, rows < 2^31
-  using AF = typename OpF::A;  // (value, column-major index)
-  static_assert(sizeof(AF) % 4 == 0, "accumulator must split into 32-bit slices");
-  constexpr int W = int(sizeof(AF) / 4);
-  constexpr int V = int(16 / sizeof(T));
-  const uint32_t b = blockIdx.x;
-  if (b < grid) {
-    A acc[KC][V];
-#pragma unroll
-    for (int k = 0; k < KC; ++k)
-#pragma unroll
-      for (int v = 0; v < V; ++v) acc[k][v] = Op::init();
-    bool own[KC];
-#pragma unroll
-    for (int k = 0; k < KC; ++k) own[k] = (uint64_t(k) * kRowBS + threadIdx.x) * V < C;  // C % V == 0
-    // rows of this block, software pipelined: the next row's loads are in flight while the
-    // current one is folded (rows arrive in increasing order, so Op::step keeps the first)
-    Vec<T, V> x[KC], y[KC];
-    auto load = [&](uint64_t r, Vec<T, V>(&dst)[KC]) {
-      const T* row = a + r * C;
-#pragma unroll
-      for (int k = 0; k < KC; ++k)
-        if (own[k]) dst[k] = vload_nt<T, V>(row + (uint64_t(k) * kRowBS + threadIdx.x) * V);
-    };
-    auto fold = [&](uint64_t r, const Vec<T, V>(&src)[KC]) {
-#pragma unroll
-      for (int k = 0; k < KC; ++k)
-        if (own[k])
-#pragma unroll
-          for (int v = 0; v < V; ++v) acc[k][v] = Op::step(acc[k][v], src[k].v[v], int64_t(r));
-    };
-    uint64_t r = b;
-    if (r < R) {
-      load(r, x);
-      for (;;) {
-        const uint64_t r1 = r + grid;
-        if (r1 >= R) {
-          fold(r, x);
-          break;
-        }
-        load(r1, y);
-        fold(r, x);
-        const uint64_t r2 = r1 + grid;
-        if (r2 >= R) {
-          fold(r1, y);
-          break;
-        }
-        load(r2, x);
-        fold(r1, y);
-        r = r2;
-      }
-    }
-    // the lane's columns -> one key; a column whose row-0 element is NaN is skipped (pass 2)
-    AF best = OpF::init();
-#pragma unroll
-    for (int k = 0; k < KC; ++k) {
-      if (!own[k]) continue;
-      const uint64_t c0 = (uint64_t(k) * kRowBS + threadIdx.x) * V;
-      const Vec<T, V> top = vload<T, V>(a + c0);  // row 0, shared by every block (cache hits)
-#pragma unroll
-      for (int v = 0; v < V; ++v)
-        if (acc[k][v].idx >= 0 && !is_nan(top.v[v]))
-          best = OpF::comb(best, AF{acc[k][v].val, int64_t(c0 + v) * int64_t(R) + int64_t(acc[k][v].idx)});
-    }
-    best = group_reduce<OpF, kRowBS>(best, R * C < 0xffffffffull);
-    if (threadIdx.x == 0) {
-      uint32_t s[W];
-      __builtin_memcpy(s, &best, sizeof(AF));
-      publish_slices<W>(fa.slots + uint64_t(b) * W, s);
-    }
-    return;
-  }
-  // combiner: lane l folds block results l, l + 512 (PER = 2 at most), then the block tree
-  constexpr int PER = 2;
-  uint64_t vv[PER][W];
-  const bool ok = gather_published<W, PER>(fa.slots, grid, fa.spin_limit, vv);
-  AF res = OpF::init();
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t bb = threadIdx.x + j * kRowBS;
-    if (bb >= grid) break;
-    uint32_t s[W];
-#pragma unroll
-    for (int i = 0; i < W; ++i) s[i] = uint32_t(vv[j][i]);
-    AF xv;
-    __builtin_memcpy(&xv, s, sizeof(AF));
-    res = OpF::comb(res, xv);
-#pragma unroll
-    for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
-  }
-  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
-  res = group_reduce<OpF, kRowBS>(res, R * C < 0xffffffffull);
-  if (threadIdx.x == 0) {
-    const T x00 = a[0];
-    if (is_nan(x00)) res = AF{x00, 0};  // column 0 is NaN: it absorbs the second pass
-    write_result<OpF, T, kWriteFinal>(out, 0, res, 0);
-  }
-}
-
-// --------------------------------------------------------------------------------------------
 // col kernel: block = (outer, column group, tile); 64 lanes x VEC columns, 4 waves split rows.
 struct ColArgs {
   RowIndexer<1> ix;   // outer output dims (all but the innermost one) -> input offset
@@ -741,6 +626,86 @@ __global__ __launch_bounds__(BS) void k_reduce_col(const T* __restrict__ a, ColA
       const uint64_t o = uint64_t(outer) * ca.C + c0 + v;
       write_result<Op, T, WRITE>(out, o * ca.tiles + t, r, int64_t(t) * int64_t(ca.chunk));
     }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// max / min over both axes of a C-contiguous (R, C) array in one launch, with the result the
+// reference's two passes give (reduce_multi, reduction.rs:118-155: axis 0 with keepdims, then
+// axis 1).  Pass 1 keeps, per column, the first row holding the column's extreme, and a column
+// whose row-0 element is NaN becomes NaN; pass 2 keeps the first column holding the extreme of
+// those columns and skips NaN ones, unless column 0 is NaN, which absorbs everything.  So the
+// result is the element of extreme value that comes first in COLUMN-major order, among the
+// non-NaN elements of the columns whose row-0 element is not NaN -- or x[0][0] when that is NaN.
+// The streaming blocks are the column kernel's (column group, row tile) blocks; wave 0 then folds
+// its lanes' columns into one (value, col * R + row) key, skipping columns whose row 0 is NaN,
+// and publishes it; the last block of the grid combines the published keys in a fixed order.
+template <class Op, class OpF, class T, int VEC, int UNROLL, int BS, int PER>
+__global__ __launch_bounds__(BS) void k_reduce_col2d(const T* __restrict__ a, ColArgs ca, uint32_t nblk, bool vec_ok,
+                                                     RedOut<T> out, FusedArgs fa) {
+  using A = typename Op::A;
+  using AF = typename OpF::A;
+  static_assert(sizeof(AF) % 4 == 0, "accumulator must split into 32-bit slices");
+  constexpr int W = int(sizeof(AF) / 4);
+  __shared__ A part[BS / kWave - 1][kWave * VEC];
+  const uint32_t b = blockIdx.x;
+  const bool idx32 = ca.R * ca.C < 0xffffffffull;
+  if (b < nblk) {
+    const uint32_t t = b % ca.tiles;
+    const uint32_t cg = b / ca.tiles;
+    // which of wave 0's columns head with a NaN (pass 2 drops them): read before the stream, so
+    // the loads overlap it
+    const uint64_t c0 = uint64_t(cg) * kWave * VEC + uint64_t(threadIdx.x % kWave) * VEC;
+    uint32_t nan_head = 0;
+    if (threadIdx.x < kWave) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (c0 + v < ca.C && is_nan(a[c0 + v])) nan_head |= 1u << v;
+    }
+    A acc[VEC];
+    T first[VEC];
+    col_partial<Op, T, VEC, UNROLL, BS>(a, ca, vec_ok, t, cg, 0, part, acc, first);
+    if (threadIdx.x < kWave) {  // wave 0 holds the block's per-column results
+      AF best = OpF::init();
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const uint64_t col = c0 + v;
+        if (col < ca.C && acc[v].idx >= 0 && !(nan_head & (1u << v)))
+          best = OpF::comb(best, AF{acc[v].val, int64_t(col) * int64_t(ca.R) + int64_t(t) * int64_t(ca.chunk) +
+                                                    int64_t(acc[v].idx)});
+      }
+      best = group_reduce<OpF, kWave>(best, idx32);
+      if (threadIdx.x == 0) {
+        uint32_t s[W];
+        __builtin_memcpy(s, &best, sizeof(AF));
+        publish_slices<W>(fa.slots + uint64_t(b) * W, s);
+      }
+    }
+    return;
+  }
+  // combiner: lane l folds keys l, l + BS, ... (PER at most), then the block tree
+  uint64_t vv[PER][W];
+  const bool ok = gather_published<W, PER, BS>(fa.slots, nblk, fa.spin_limit, vv);
+  AF res = OpF::init();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t bb = threadIdx.x + j * BS;
+    if (bb >= nblk) break;
+    uint32_t s[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) s[i] = uint32_t(vv[j][i]);
+    AF xv;
+    __builtin_memcpy(&xv, s, sizeof(AF));
+    res = OpF::comb(res, xv);
+#pragma unroll
+    for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
+  }
+  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
+  res = group_reduce<OpF, BS>(res, idx32);
+  if (threadIdx.x == 0) {
+    const T x00 = a[0];
+    if (is_nan(x00)) res = AF{x00, 0};  // column 0 is NaN: it absorbs the second pass
+    write_result<OpF, T, kWriteFinal>(out, 0, res, 0);
   }
 }
 
@@ -1039,28 +1004,45 @@ int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid
 }
 
 
-// max / min over both axes of a C-contiguous, 16-byte aligned (R, C) array in one launch
-// (k_reduce_2d_ordered); kFusedNotCovered when the shape does not fit it
+// max / min over both axes of a C-contiguous (R, C) array in one launch (k_reduce_col2d), with
+// the column kernel's tiling (about 256 blocks); kFusedNotCovered when the shape does not fit it
 template <class Op, class OpF, class T>
 int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, void* ws, size_t ws_bytes,
                              hipStream_t st) {
   constexpr int V = rvec<T>();
-  if (R == 0 || C == 0 || ws == nullptr || !al16(a) || C % V || R >= (uint64_t(1) << 31)) return kFusedNotCovered;
-  const uint64_t kc = ceil_div(C, uint64_t(kRowBS) * V);
-  if (kc > 4 || R * C >= (uint64_t(1) << 62)) return kFusedNotCovered;
-  const uint32_t grid = uint32_t(R < 2 * kRowBS ? R : 2 * kRowBS);  // the combiner folds up to 2 * 512 slots
+  constexpr int BS = 256;
+  if (R == 0 || C == 0 || ws == nullptr || R >= (uint64_t(1) << 31) || R * C >= (uint64_t(1) << 62))
+    return kFusedNotCovered;
+  ColArgs ca{};
+  ca.nt = true;
+  ca.ix.nd = 0;
+  ca.C = C;
+  ca.cgroups = uint32_t(ceil_div(C, uint64_t(kWave) * V));
+  ca.R = R;
+  ca.rs = int64_t(C);
+  // about 256 long-lived blocks, as the column kernel (128: 67 us, 256: 54 us, 512: 53.5 us,
+  // 1024: 61 us for (8192, 8192) f32 max)
+  uint64_t tiles = ca.cgroups >= 256 ? 1 : ceil_div(256, ca.cgroups);
+  const uint64_t max_tiles = ceil_div(R, 64);
+  if (tiles > max_tiles) tiles = max_tiles;
+  if (tiles < 1) tiles = 1;
+  if (uint64_t(ca.cgroups) * tiles > 4 * BS) return kFusedNotCovered;  // the combiner folds up to 1024 keys
+  ca.chunk = ceil_div(R, tiles);
+  ca.tiles = uint32_t(tiles);
+  const uint32_t nblk = uint32_t(uint64_t(ca.cgroups) * tiles);
+  const bool vec_ok = al16(a) && (C % V == 0) && (C * sizeof(T)) % 16 == 0;
   const uint64_t W = sizeof(typename OpF::A) / 4;
-  if (uint64_t(grid) * W * 8 > ws_bytes) return kFusedNoRoom;
+  if (uint64_t(nblk) * W * 8 > ws_bytes) return kFusedNoRoom;
   FusedArgs fa{};
   fa.slots = static_cast<uint64_t*>(ws);
   fa.fault = device_fault_word(st);
   fa.spin_limit = wait_spin_limit();
   if (fa.fault == nullptr) return kFusedNotCovered;
-  const dim3 g(grid + 1);
-  switch (kc) {
-    case 1: k_reduce_2d_ordered<Op, OpF, T, 1><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
-    case 2: k_reduce_2d_ordered<Op, OpF, T, 2><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
-    default: k_reduce_2d_ordered<Op, OpF, T, 4><<<g, kRowBS, 0, st>>>(a, R, C, grid, out, fa); break;
+  const dim3 g(nblk + 1);
+  switch (ceil_div(nblk, uint64_t(BS))) {
+    case 1: k_reduce_col2d<Op, OpF, T, V, 8, BS, 1><<<g, BS, 0, st>>>(a, ca, nblk, vec_ok, out, fa); break;
+    case 2: k_reduce_col2d<Op, OpF, T, V, 8, BS, 2><<<g, BS, 0, st>>>(a, ca, nblk, vec_ok, out, fa); break;
+    default: k_reduce_col2d<Op, OpF, T, V, 8, BS, 4><<<g, BS, 0, st>>>(a, ca, nblk, vec_ok, out, fa); break;
   }
   return kFusedLaunched;
 }
