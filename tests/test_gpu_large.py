@@ -51,3 +51,28 @@ def test_reversed_copy_past_2_32_elements():
     gc.collect()
     ms.synchronize()
     ms.empty_cache()
+
+
+def test_zero_ties_past_2_31_elements():
+    """The whole-array reduction's packed 64-bit wave keys (value, ~index) hold indices below
+    2^32 - 1: a zero tie past 2^31 must still go to the lower index and keep that zero's sign."""
+    n = (1 << 31) + (1 << 20)
+    x = np.full(n, -1.0, np.float32)
+    lo, hi = (1 << 31) + 123, (1 << 31) + 456
+    x[lo], x[hi] = -0.0, 0.0
+    X = ms.from_numpy(x)
+    del x
+    assert ms.argmax(X).item() == lo
+    assert np.signbit(ms.max(X).numpy())  # the first zero is -0
+    del X
+    gc.collect()
+    y = np.full(n, 1.0, np.float32)
+    y[lo], y[hi] = 0.0, -0.0
+    Y = ms.from_numpy(y)
+    del y
+    assert ms.argmin(Y).item() == lo
+    assert not np.signbit(ms.min(Y).numpy())  # the first zero is +0
+    del Y
+    gc.collect()
+    ms.synchronize()
+    ms.empty_cache()

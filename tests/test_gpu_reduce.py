@@ -437,3 +437,23 @@ def test_two_axis_single_launch(kind, dt):
         check_reduce(kind, y, (0, 1))
         y[0, 0] = np.nan                   # absorbs everything
         check_reduce(kind, y, (0, 1))
+
+
+@pytest.mark.parametrize("kind", ["max", "min", "argmax", "argmin"])
+def test_whole_array_signed_zero_ties(kind):
+    """Whole-array f32 reductions of 3M+ elements (the persistent grid with its packed-key wave
+    combine, in the streaming blocks and in the combiner): when the extreme is a zero, the first
+    zero decides the index and the sign, whether -0 or +0 comes first, with the first zero in a
+    late block."""
+    n = 3_000_000 + 77
+    fill = np.float32(-1.0 if kind in ("max", "argmax") else 1.0)
+    for first, second in ((-0.0, 0.0), (0.0, -0.0)):
+        x = np.full(n, fill, np.float32)
+        x[2_500_001], x[2_900_000] = first, second
+        check_reduce(kind, x, None)
+        x[1_000_003] = second  # now the first zero sits in an earlier block
+        check_reduce(kind, x, None)
+    x = np.full(n, fill, np.float32)
+    idx = RNG.choice(np.arange(1_000_000, n), 5000, replace=False)
+    x[idx] = np.where(RNG.random(5000) < 0.5, -0.0, 0.0).astype(np.float32)
+    check_reduce(kind, x, None)
