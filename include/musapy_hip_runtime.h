@@ -76,6 +76,34 @@ void mpy_rt_mem_stats(size_t* live_bytes, size_t* peak_bytes, size_t* num_allocs
 /* Writes `nbytes` of a pattern to `ptr` with a kernel (graph-capture safe, unlike memset). */
 int mpy_rt_fill_u32(void* ptr, uint32_t value, size_t nbytes, hipStream_t stream);
 
+/* The device wait-fault word of the kernel library (musapy_kernels_take_fault), read through the
+ * runtime so that tests can inject it: 0, a fault bit set, or -1. */
+int mpy_rt_take_fault(int device);
+
+/* ---- test hooks (counterpart of the reference's mock runtime, musa_ffi.rs:154-355) ----
+ * mpy_rt_set_backend(MPY_RT_BACKEND_HOST) swaps every HIP call of this layer for a host fake:
+ * one device, memory from the C heap, copies as memcpy, streams and events as tokens,
+ * synchronizes immediate, kernel launches without effect (their results are meaningless).  It
+ * lets CPU-only tests drive the op layer's error paths.  It is refused (hipErrorNotSupported) on
+ * a machine with a HIP device, where the kernels would be handed host pointers, and while memory
+ * of the other backend is held.
+ * mpy_rt_inject(call, code, skip, count): after `skip` more calls of the class, the next `count`
+ * calls fail with `code` (a hipError_t; for MPY_RT_CALL_FAULT the fault bits to report), on
+ * either backend.  count 0 disarms it. */
+enum { MPY_RT_BACKEND_HIP = 0, MPY_RT_BACKEND_HOST = 1 };
+enum {
+  MPY_RT_CALL_MALLOC = 0, /* device allocation misses (hipMalloc) */
+  MPY_RT_CALL_MEMCPY,     /* host<->device and device copies */
+  MPY_RT_CALL_SYNC,       /* stream, device and event synchronizes */
+  MPY_RT_CALL_LAUNCH,     /* the launch-error check after a kernel-ABI call */
+  MPY_RT_CALL_FAULT,      /* the device wait-fault word read after a synchronize */
+  MPY_RT_CALL_EVENT,      /* event create / record / stream wait */
+  MPY_RT_CALL_STREAM,     /* stream create */
+  MPY_RT_CALL_COUNT
+};
+int mpy_rt_set_backend(int backend);
+int mpy_rt_inject(int call, int code, int skip, int count);
+
 #ifdef __cplusplus
 }
 #endif

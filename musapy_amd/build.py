@@ -97,10 +97,87 @@ def build(jobs: int | None = None, verbose: bool = True) -> None:
         print(f"built {lib_path()} and {core_path()}")
 
 
+# ---- sanitized host build (CPU tests of the host code) ----------------------------------------
+# The kernel sources are compiled for the host side only (no device code, so kernel launches fail
+# at run time exactly as they do on a machine without a GPU); the host code of every source is
+# built with AddressSanitizer + UndefinedBehaviorSanitizer by clang, so one sanitizer runtime
+# (clang's) serves the whole process.  The result is a copy of the package under
+# ``_build/sanitized/musapy_amd``; it is meant for the host-memory runtime backend
+# (mpy_rt_set_backend) and must be loaded with clang's ASan runtime preloaded
+# (``sanitizer_env()``).
+CLANGXX = os.path.join(ROCM, "llvm", "bin", "clang++")
+SAN_HIP_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined"]
+SAN_CXX_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+SAN_COMMON = ["-O1", "-g", "-std=c++17", "-fPIC", "-fno-omit-frame-pointer", "-ffp-contract=off"]
+
+
+def sanitized_dir() -> str:
+    return os.path.join(BUILD, "sanitized")
+
+
+def asan_runtime() -> str:
+    r = subprocess.run([CLANGXX, "-print-file-name=libclang_rt.asan-x86_64.so"], stdout=subprocess.PIPE, text=True)
+    path = r.stdout.strip()
+    if r.returncode != 0 or not os.path.isfile(path):
+        raise RuntimeError("clang's ASan runtime (libclang_rt.asan-x86_64.so) was not found")
+    return path
+
+
+def sanitizer_env(env: dict | None = None) -> dict:
+    """Environment for a Python process that imports the sanitized package."""
+    env = dict(os.environ if env is None else env)
+    env["LD_PRELOAD"] = asan_runtime()
+    # the interpreter and HIP's runtime are not instrumented; their allocations are not ours
+    env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=0:halt_on_error=1:exitcode=86"
+    env["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1:exitcode=87"
+    env["PYTHONPATH"] = sanitized_dir() + os.pathsep + env.get("PYTHONPATH", "")
+    return env
+
+
+def build_sanitized(jobs: int | None = None, verbose: bool = True) -> str:
+    import pybind11
+
+    out = os.path.join(sanitized_dir(), "musapy_amd")
+    objdir = os.path.join(sanitized_dir(), "obj")
+    os.makedirs(out, exist_ok=True)
+    os.makedirs(objdir, exist_ok=True)
+    incs = [f"-I{pybind11.get_include()}", f"-I{sysconfig.get_paths()['include']}"]
+
+    def obj(src: str) -> str:
+        return os.path.join(objdir, src.replace("/", "_") + ".o")
+
+    def hip(src: str) -> str:
+        _run([HIPCC, f"--offload-arch={ARCH}", *SAN_HIP_FLAGS, *SAN_COMMON, "-x", "hip", "-c",
+              os.path.join(CSRC, src), "-o", obj(src)])
+        return obj(src)
+
+    def cxx(src: str) -> str:
+        _run([CLANGXX, *SAN_CXX_FLAGS, *SAN_COMMON, *incs, "-c", os.path.join(CSRC, src), "-o", obj(src)])
+        return obj(src)
+
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        hip_objs = [f.result() for f in [ex.submit(hip, s) for s in HIP_SOURCES]]
+        cxx_objs = [f.result() for f in [ex.submit(cxx, s) for s in CXX_SOURCES]]
+    lib = os.path.join(out, "libmusapy_hip.so")
+    _run([CLANGXX, *SAN_CXX_FLAGS, "-shared-libsan", "-shared", "-o", lib, *hip_objs, f"-L{ROCM}/lib",
+          "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
+    core = os.path.join(out, os.path.basename(core_path()))
+    _run([CLANGXX, *SAN_CXX_FLAGS, "-shared-libsan", "-shared", "-o", core, *cxx_objs, f"-L{out}", "-lmusapy_hip",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"])
+    shutil.copyfile(os.path.join(PKG, "__init__.py"), os.path.join(out, "__init__.py"))
+    if verbose:
+        print(f"built the sanitized host package in {out}")
+    return out
+
+
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
 
 
 if __name__ == "__main__":
-    build()
+    if "--sanitized" in sys.argv[1:]:
+        build_sanitized()
+    else:
+        build()
     sys.exit(0)

@@ -1369,7 +1369,7 @@ int musapy_kernels_take_fault(int device) {
     }
   }
   if (result < 0) (void)hipGetLastError();
-  if (device != prev) hipSetDevice(prev);
+  if (device != prev) (void)hipSetDevice(prev);
   return result;
 }
 

@@ -7,7 +7,6 @@
 #include <mutex>
 
 #include "../../../include/musapy_hip_runtime.h"
-#include "../../../include/musapy_kernels.h"
 
 namespace mpy {
 namespace ops {
@@ -170,9 +169,10 @@ Layout Layout::flipped(size_t axis) const {
   if (axis >= ndim())
     throw ShapeError("flip axis " + std::to_string(axis) + " out of bounds for ndim " + std::to_string(ndim()));
   Layout r = *this;
-  ssize_t off = ssize_t(offset) + (ssize_t(shape[axis]) - 1) * strides[axis];
   r.strides[axis] = -strides[axis];
-  r.offset = size_t(off);
+  // the offset moves to the axis' last element (layout.rs:183-205); an empty axis has none, and
+  // its view keeps the offset rather than wrapping it below zero as the reference's does
+  if (shape[axis] > 0) r.offset = size_t(ssize_t(offset) + (ssize_t(shape[axis]) - 1) * strides[axis]);
   return r;
 }
 
@@ -252,7 +252,7 @@ void Stream::synchronize() {
   }
   if (!wait_check_) return;
   wait_check_ = false;
-  const int fault = musapy_kernels_take_fault(device_);
+  const int fault = mpy_rt_take_fault(device_);
   if (fault == 0) return;
   poisoned_ = true;
   if (fault < 0) throw StreamError("stream synchronize: the device's wait-fault word could not be read");
@@ -298,9 +298,10 @@ void stream_wait_stream(const StreamPtr& waiter, const StreamPtr& target) {
   if (!waiter || !target || waiter.get() == target.get()) return;
   hipEvent_t ev = nullptr;
   check_rt(mpy_rt_event_create(&ev, 0), "event create");
-  check_rt(mpy_rt_event_record(ev, target->raw()), "event record");
-  check_rt(mpy_rt_stream_wait_event(waiter->raw(), ev), "stream wait event");
-  mpy_rt_event_destroy(ev);
+  int e = mpy_rt_event_record(ev, target->raw());
+  if (e == 0) e = mpy_rt_stream_wait_event(waiter->raw(), ev);
+  mpy_rt_event_destroy(ev);  // also when the record or the wait failed
+  check_rt(e, "stream wait event");
 }
 }  // namespace
 
@@ -344,11 +345,19 @@ Buffer::~Buffer() {
     return;
   }
   if (!ptr_) return;
-  try {
-    if (last_writer_) stream_wait_stream(home_, last_writer_);
-    for (auto& r : readers_) stream_wait_stream(home_, r);
-  } catch (...) {
-  }
+  // the free is ordered on the home stream: order it after the other streams' use first, or,
+  // where that cannot be done (no home stream, a failing event call), wait for them on the host
+  auto order_after = [this](const StreamPtr& s) {
+    if (!s || (home_ && s.get() == home_.get())) return;
+    try {
+      if (!home_) throw StreamError("no home stream");
+      stream_wait_stream(home_, s);
+    } catch (...) {
+      mpy_rt_stream_synchronize(s->raw());
+    }
+  };
+  order_after(last_writer_);
+  for (auto& r : readers_) order_after(r);
   mpy_rt_free(ptr_, home_ ? home_->raw() : nullptr);
 }
 

@@ -19,9 +19,18 @@
 // the device drains (host time per op equal to its GPU time), which is what this avoids.
 // All functions return 0 on success or a hipError_t code.  Streams are always created with the
 // default priority.
+//
+// Every HIP call goes through a call table (Calls).  The default table calls HIP.  Tests can
+// swap in a host-memory table (mpy_rt_set_backend) that runs the whole op layer on a machine
+// without a GPU -- device memory is host memory, copies are memcpy, streams and events are
+// tokens, kernel launches do nothing -- and can arm one-shot errors on any call class
+// (mpy_rt_inject), on either table.  This is the counterpart of the reference's mock runtime
+// (rust/musapy-core/src/musa_ffi.rs:154-355) for testing the error paths: launch errors,
+// synchronize errors, device wait faults, allocation failures.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -29,13 +38,162 @@
 #include <vector>
 
 #include "../../../include/musapy_hip_runtime.h"
-
-extern "C" int musapy_kernels_take_error(void);
+#include "../../../include/musapy_kernels.h"
 
 namespace {
 
 constexpr int kMaxDevices = 64;
 
+// ---------------------------------------------------------------------------------------------
+// the call table
+struct Calls {
+  hipError_t (*device_count)(int*);
+  hipError_t (*set_device)(int);
+  hipError_t (*get_device)(int*);
+  hipError_t (*device_info)(int, char*, size_t, size_t*, int*, int*, int*);
+  hipError_t (*malloc)(void**, size_t);
+  hipError_t (*free)(void*);
+  hipError_t (*memcpy_async)(void*, const void*, size_t, hipMemcpyKind, hipStream_t);
+  hipError_t (*stream_create)(hipStream_t*);
+  hipError_t (*stream_destroy)(hipStream_t);
+  hipError_t (*stream_sync)(hipStream_t);
+  hipError_t (*device_sync)();
+  hipError_t (*event_create)(hipEvent_t*, unsigned);
+  hipError_t (*event_destroy)(hipEvent_t);
+  hipError_t (*event_record)(hipEvent_t, hipStream_t);
+  hipError_t (*stream_wait_event)(hipStream_t, hipEvent_t);
+  hipError_t (*event_sync)(hipEvent_t);
+  hipError_t (*event_elapsed)(float*, hipEvent_t, hipEvent_t);
+  hipError_t (*last_error)();  // the pending launch error, consumed
+  hipError_t (*fill_u32)(void*, uint32_t, size_t, hipStream_t);
+  int (*take_fault)(int);      // the kernel library's device wait-fault word
+};
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) p[i] = v;
+}
+
+hipError_t hip_device_info(int device, char* name, size_t name_len, size_t* total_mem, int* cu_count, int* major,
+                           int* minor) {
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return e;
+  if (name && name_len) {
+    std::strncpy(name, prop.gcnArchName, name_len - 1);
+    name[name_len - 1] = 0;
+  }
+  if (total_mem) *total_mem = prop.totalGlobalMem;
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (major) *major = prop.major;
+  if (minor) *minor = prop.minor;
+  return hipSuccess;
+}
+
+const Calls kHipCalls = {
+    [](int* n) { return hipGetDeviceCount(n); },
+    [](int d) { return hipSetDevice(d); },
+    [](int* d) { return hipGetDevice(d); },
+    hip_device_info,
+    [](void** p, size_t n) { return hipMalloc(p, n); },
+    [](void* p) { return hipFree(p); },
+    [](void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t st) { return hipMemcpyAsync(d, s, n, k, st); },
+    [](hipStream_t* s) { return hipStreamCreateWithFlags(s, hipStreamNonBlocking); },
+    [](hipStream_t s) { return hipStreamDestroy(s); },
+    [](hipStream_t s) { return hipStreamSynchronize(s); },
+    []() { return hipDeviceSynchronize(); },
+    [](hipEvent_t* e, unsigned f) { return hipEventCreateWithFlags(e, f); },
+    [](hipEvent_t e) { return hipEventDestroy(e); },
+    [](hipEvent_t e, hipStream_t s) { return hipEventRecord(e, s); },
+    [](hipStream_t s, hipEvent_t e) { return hipStreamWaitEvent(s, e, 0); },
+    [](hipEvent_t e) { return hipEventSynchronize(e); },
+    [](float* ms, hipEvent_t a, hipEvent_t b) { return hipEventElapsedTime(ms, a, b); },
+    []() { return hipGetLastError(); },
+    [](void* p, uint32_t v, size_t nbytes, hipStream_t st) {
+      const size_t n = nbytes / 4;
+      if (n == 0) return hipSuccess;
+      size_t g = (n + 255) / 256;
+      if (g > 65536) g = 65536;
+      k_fill_u32<<<dim3(unsigned(g)), 256, 0, st>>>(static_cast<uint32_t*>(p), v, n);
+      return hipGetLastError();
+    },
+    [](int d) { return musapy_kernels_take_fault(d); },
+};
+
+// The host-memory table: one fake device, memory from the C heap, streams and events as tokens,
+// every synchronize immediate, kernel launches without effect (the pending HIP error of a launch
+// that found no device is consumed and not reported).
+std::atomic<uintptr_t> g_fake_token{0x1000};
+const Calls kHostCalls = {
+    [](int* n) { *n = 1; return hipSuccess; },
+    [](int d) { return d == 0 ? hipSuccess : hipErrorInvalidDevice; },
+    [](int* d) { *d = 0; return hipSuccess; },
+    [](int d, char* name, size_t len, size_t* mem, int* cus, int* major, int* minor) {
+      if (d != 0) return hipErrorInvalidDevice;
+      if (name && len) {
+        std::strncpy(name, "host-fake", len - 1);
+        name[len - 1] = 0;
+      }
+      if (mem) *mem = size_t(1) << 34;
+      if (cus) *cus = 1;
+      if (major) *major = 9;
+      if (minor) *minor = 5;
+      return hipSuccess;
+    },
+    [](void** p, size_t n) {
+      *p = std::aligned_alloc(256, (n + 255) / 256 * 256);
+      return *p ? hipSuccess : hipErrorOutOfMemory;
+    },
+    [](void* p) { std::free(p); return hipSuccess; },
+    [](void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) { std::memmove(d, s, n); return hipSuccess; },
+    [](hipStream_t* s) { *s = reinterpret_cast<hipStream_t>(g_fake_token.fetch_add(16)); return hipSuccess; },
+    [](hipStream_t) { return hipSuccess; },
+    [](hipStream_t) { return hipSuccess; },
+    []() { return hipSuccess; },
+    [](hipEvent_t* e, unsigned) { *e = reinterpret_cast<hipEvent_t>(g_fake_token.fetch_add(16)); return hipSuccess; },
+    [](hipEvent_t) { return hipSuccess; },
+    [](hipEvent_t, hipStream_t) { return hipSuccess; },
+    [](hipStream_t, hipEvent_t) { return hipSuccess; },
+    [](hipEvent_t) { return hipSuccess; },
+    [](float* ms, hipEvent_t, hipEvent_t) { *ms = 0.0f; return hipSuccess; },
+    []() { (void)hipGetLastError(); return hipSuccess; },
+    [](void* p, uint32_t v, size_t nbytes, hipStream_t) {
+      uint32_t* q = static_cast<uint32_t*>(p);
+      for (size_t i = 0; i < nbytes / 4; ++i) q[i] = v;
+      return hipSuccess;
+    },
+    [](int) { return 0; },
+};
+
+std::atomic<const Calls*> g_calls{&kHipCalls};
+inline const Calls& H() { return *g_calls.load(std::memory_order_acquire); }
+
+// one-shot error injection: after `skip` more calls of the class, the next `count` calls return
+// `code` (for MPY_RT_CALL_FAULT: report `code` as the fault word) instead of doing their work
+struct Injection {
+  std::atomic<int> code{0}, skip{0}, count{0};
+};
+Injection g_inject[MPY_RT_CALL_COUNT];
+
+// true (and the code in *code) when this call of `cls` is to fail
+bool injected(int cls, int* code) {
+  Injection& in = g_inject[cls];
+  if (in.count.load(std::memory_order_relaxed) <= 0) return false;
+  if (in.skip.load(std::memory_order_relaxed) > 0) {
+    in.skip.fetch_sub(1);
+    return false;
+  }
+  if (in.count.fetch_sub(1) <= 0) return false;
+  *code = in.code.load();
+  return true;
+}
+
+#define MPY_INJECT(CLS)                                      \
+  do {                                                       \
+    int code_ = 0;                                           \
+    if (injected(CLS, &code_)) return rc(hipError_t(code_)); \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------
 struct Block {
   void* ptr;
   size_t size;         // size class actually allocated
@@ -73,18 +231,18 @@ void note_alloc(size_t n) {
 // "last error", which the next launch check would report against an unrelated kernel; the
 // caller is told here instead, so the sticky copy is consumed.
 int rc(hipError_t e) {
-  if (e != hipSuccess) (void)hipGetLastError();
+  if (e != hipSuccess) (void)H().last_error();
   return int(e);
 }
 
 // make `waiter` wait for everything queued so far on `target`
 hipError_t order_after(hipStream_t waiter, hipStream_t target) {
   hipEvent_t ev = nullptr;
-  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  hipError_t e = H().event_create(&ev, hipEventDisableTiming);
   if (e != hipSuccess) return e;
-  e = hipEventRecord(ev, target);
-  if (e == hipSuccess) e = hipStreamWaitEvent(waiter, ev, 0);
-  hipEventDestroy(ev);
+  e = H().event_record(ev, target);
+  if (e == hipSuccess) e = H().stream_wait_event(waiter, ev);
+  H().event_destroy(ev);
   return e;
 }
 
@@ -93,43 +251,28 @@ hipError_t release_cached_locked(int device) {
   DevicePool& P = g_pools[device];
   if (P.free.empty()) return hipSuccess;
   int prev = 0;
-  hipGetDevice(&prev);
-  hipError_t e = hipSetDevice(device);
+  H().get_device(&prev);
+  hipError_t e = H().set_device(device);
   if (e != hipSuccess) return e;
-  e = hipDeviceSynchronize();  // frees were stream-ordered: their work must be done
-  for (auto& kv : P.free) hipFree(kv.second.ptr);
+  e = H().device_sync();  // frees were stream-ordered: their work must be done
+  for (auto& kv : P.free) H().free(kv.second.ptr);
   P.free.clear();
   P.cached_bytes = 0;
-  hipSetDevice(prev);
+  H().set_device(prev);
   return e;
-}
-
-__global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) p[i] = v;
 }
 
 }  // namespace
 
 extern "C" {
 
-int mpy_rt_device_count(int* count) { return rc(hipGetDeviceCount(count)); }
+int mpy_rt_device_count(int* count) { return rc(H().device_count(count)); }
 
-int mpy_rt_set_device(int device) { return rc(hipSetDevice(device)); }
+int mpy_rt_set_device(int device) { return rc(H().set_device(device)); }
 
 int mpy_rt_device_info(int device, char* name, size_t name_len, size_t* total_mem, int* cu_count, int* arch_major,
                        int* arch_minor) {
-  hipDeviceProp_t prop;
-  hipError_t e = hipGetDeviceProperties(&prop, device);
-  if (e != hipSuccess) return rc(e);
-  if (name && name_len) {
-    std::strncpy(name, prop.gcnArchName, name_len - 1);
-    name[name_len - 1] = 0;
-  }
-  if (total_mem) *total_mem = prop.totalGlobalMem;
-  if (cu_count) *cu_count = prop.multiProcessorCount;
-  if (arch_major) *arch_major = prop.major;
-  if (arch_minor) *arch_minor = prop.minor;
-  return 0;
+  return rc(H().device_info(device, name, name_len, total_mem, cu_count, arch_major, arch_minor));
 }
 
 int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
@@ -168,16 +311,17 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
     *ptr = b.ptr;
     return 0;
   }
-  hipError_t e = hipSetDevice(device);
+  hipError_t e = H().set_device(device);
   if (e != hipSuccess) return rc(e);
   void* p = nullptr;
-  e = hipMalloc(&p, cls);
+  int code = 0;
+  e = injected(MPY_RT_CALL_MALLOC, &code) ? hipError_t(code) : H().malloc(&p, cls);
   if (e == hipErrorOutOfMemory) {
-    (void)hipGetLastError();
+    (void)H().last_error();
     for (int d = 0; d < kMaxDevices; ++d)
       if (!g_pools[d].free.empty()) release_cached_locked(d);
-    hipSetDevice(device);
-    e = hipMalloc(&p, cls);
+    H().set_device(device);
+    e = injected(MPY_RT_CALL_MALLOC, &code) ? hipError_t(code) : H().malloc(&p, cls);
   }
   if (e != hipSuccess) return rc(e);
   P.live[p] = Block{p, cls, nbytes, stream, false};
@@ -202,7 +346,7 @@ int mpy_rt_free(void* ptr, hipStream_t stream) {
     P.cached_bytes += b.size;
     return 0;
   }
-  return rc(hipFree(ptr));  // not from this allocator
+  return rc(H().free(ptr));  // not from this allocator
 }
 
 int mpy_rt_empty_cache(int device) {
@@ -218,30 +362,34 @@ int mpy_rt_empty_cache(int device) {
 
 int mpy_rt_memcpy_h2d(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
-  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s);
+  MPY_INJECT(MPY_RT_CALL_MEMCPY);
+  hipError_t e = H().memcpy_async(dst, src, n, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return rc(e);
-  return rc(hipStreamSynchronize(s));  // the host buffer may be released right after
+  return rc(H().stream_sync(s));  // the host buffer may be released right after
 }
 int mpy_rt_memcpy_d2h(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
-  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s);
+  MPY_INJECT(MPY_RT_CALL_MEMCPY);
+  hipError_t e = H().memcpy_async(dst, src, n, hipMemcpyDeviceToHost, s);
   if (e != hipSuccess) return rc(e);
-  return rc(hipStreamSynchronize(s));
+  return rc(H().stream_sync(s));
 }
 int mpy_rt_memcpy_d2d(void* dst, const void* src, size_t n, hipStream_t s) {
   if (n == 0) return 0;
-  return rc(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s));
+  MPY_INJECT(MPY_RT_CALL_MEMCPY);
+  return rc(H().memcpy_async(dst, src, n, hipMemcpyDeviceToDevice, s));
 }
 
 int mpy_rt_stream_create(hipStream_t* stream, int device) {
-  hipError_t e = hipSetDevice(device);
+  MPY_INJECT(MPY_RT_CALL_STREAM);
+  hipError_t e = H().set_device(device);
   if (e != hipSuccess) return rc(e);
-  return rc(hipStreamCreateWithFlags(stream, hipStreamNonBlocking));
+  return rc(H().stream_create(stream));
 }
 int mpy_rt_stream_destroy(hipStream_t stream) {
   // cached blocks last freed on this stream outlive it: drain it, then mark them idle so no
   // later reuse records an event on the destroyed handle
-  hipError_t e = hipStreamSynchronize(stream);
+  hipError_t e = H().stream_sync(stream);
   {
     std::lock_guard<std::mutex> lk(g_mu);
     for (int d = 0; d < kMaxDevices; ++d) {
@@ -251,26 +399,50 @@ int mpy_rt_stream_destroy(hipStream_t stream) {
         if (kv.second.stream == stream) kv.second.idle = true;
     }
   }
-  hipError_t e2 = hipStreamDestroy(stream);
+  hipError_t e2 = H().stream_destroy(stream);
   return rc(e != hipSuccess ? e : e2);
 }
-int mpy_rt_stream_synchronize(hipStream_t stream) { return rc(hipStreamSynchronize(stream)); }
-int mpy_rt_device_synchronize(void) { return rc(hipDeviceSynchronize()); }
+int mpy_rt_stream_synchronize(hipStream_t stream) {
+  MPY_INJECT(MPY_RT_CALL_SYNC);
+  return rc(H().stream_sync(stream));
+}
+int mpy_rt_device_synchronize(void) {
+  MPY_INJECT(MPY_RT_CALL_SYNC);
+  return rc(H().device_sync());
+}
 
 int mpy_rt_event_create(hipEvent_t* ev, int timing) {
-  return rc(hipEventCreateWithFlags(ev, timing ? hipEventDefault : hipEventDisableTiming));
+  MPY_INJECT(MPY_RT_CALL_EVENT);
+  return rc(H().event_create(ev, timing ? hipEventDefault : hipEventDisableTiming));
 }
-int mpy_rt_event_destroy(hipEvent_t ev) { return rc(hipEventDestroy(ev)); }
-int mpy_rt_event_record(hipEvent_t ev, hipStream_t s) { return rc(hipEventRecord(ev, s)); }
-int mpy_rt_stream_wait_event(hipStream_t s, hipEvent_t ev) { return rc(hipStreamWaitEvent(s, ev, 0)); }
-int mpy_rt_event_synchronize(hipEvent_t ev) { return rc(hipEventSynchronize(ev)); }
-int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t a, hipEvent_t b) { return rc(hipEventElapsedTime(ms, a, b)); }
+int mpy_rt_event_destroy(hipEvent_t ev) { return rc(H().event_destroy(ev)); }
+int mpy_rt_event_record(hipEvent_t ev, hipStream_t s) {
+  MPY_INJECT(MPY_RT_CALL_EVENT);
+  return rc(H().event_record(ev, s));
+}
+int mpy_rt_stream_wait_event(hipStream_t s, hipEvent_t ev) {
+  MPY_INJECT(MPY_RT_CALL_EVENT);
+  return rc(H().stream_wait_event(s, ev));
+}
+int mpy_rt_event_synchronize(hipEvent_t ev) {
+  MPY_INJECT(MPY_RT_CALL_SYNC);
+  return rc(H().event_sync(ev));
+}
+int mpy_rt_event_elapsed_ms(float* ms, hipEvent_t a, hipEvent_t b) { return rc(H().event_elapsed(ms, a, b)); }
 
 int mpy_rt_check_launch(void) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return rc(e);
+  hipError_t e = H().last_error();
+  int code = 0;
+  if (injected(MPY_RT_CALL_LAUNCH, &code)) e = hipError_t(code);
+  if (e != hipSuccess) return int(e);
   const int w = musapy_kernels_take_error();
   return w ? -w : 0;
+}
+
+int mpy_rt_take_fault(int device) {
+  int code = 0;
+  if (injected(MPY_RT_CALL_FAULT, &code)) return code;
+  return H().take_fault(device);
 }
 
 const char* mpy_rt_error_string(int code) {
@@ -298,12 +470,34 @@ size_t mpy_rt_mem_cached(int device) {
 }
 
 int mpy_rt_fill_u32(void* ptr, uint32_t value, size_t nbytes, hipStream_t stream) {
-  size_t n = nbytes / 4;
-  if (n == 0) return 0;
-  size_t g = (n + 255) / 256;
-  if (g > 65536) g = 65536;
-  k_fill_u32<<<dim3(unsigned(g)), 256, 0, stream>>>(static_cast<uint32_t*>(ptr), value, n);
-  return int(hipGetLastError());
+  return rc(H().fill_u32(ptr, value, nbytes, stream));
+}
+
+int mpy_rt_set_backend(int backend) {
+  if (backend != MPY_RT_BACKEND_HIP && backend != MPY_RT_BACKEND_HOST) return int(hipErrorInvalidValue);
+  if (backend == MPY_RT_BACKEND_HOST) {
+    // kernels still launch under the fake (they find no device and do nothing); with a real GPU
+    // they would be handed host pointers, so the fake is refused wherever a device exists
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    (void)hipGetLastError();
+    if (e == hipSuccess && n > 0) return int(hipErrorNotSupported);
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int d = 0; d < kMaxDevices; ++d)
+    if (!g_pools[d].live.empty() || !g_pools[d].free.empty()) return int(hipErrorNotSupported);  // memory of the other backend
+  g_calls.store(backend == MPY_RT_BACKEND_HOST ? &kHostCalls : &kHipCalls, std::memory_order_release);
+  return 0;
+}
+
+int mpy_rt_inject(int call, int code, int skip, int count) {
+  if (call < 0 || call >= MPY_RT_CALL_COUNT || count < 0 || skip < 0) return int(hipErrorInvalidValue);
+  Injection& in = g_inject[call];
+  in.count.store(0);
+  in.code.store(code);
+  in.skip.store(skip);
+  in.count.store(count);
+  return 0;
 }
 
 }  // extern "C"
