@@ -18,6 +18,7 @@
 #include "../../../include/musapy_kernels.h"
 
 #include <atomic>
+#include <type_traits>
 #include <mutex>
 
 namespace mpy {
@@ -76,39 +77,49 @@ __device__ inline typename Op::A absorb_first(typename Op::A acc, T first) {
 }
 
 // --------------------------------------------------------------------------------------------
-// A whole wave's f32 max/min accumulators whose indices are below 2^32 - 1 (tile-relative int32,
-// or absolute int64 in a whole-array reduction of fewer elements), combined by one
-// unsigned 64-bit max per butterfly step instead of Op::comb on (value, index).  The key's high
-// word orders the values (sign-magnitude bits mapped to unsigned order, inverted for min), its
-// low word is ~index, so among equal values the lowest index wins, and an empty accumulator
-// (key 0) loses to every element.  +0 and -0 compare equal and so share a key (the +0 bits); when
-// a zero wins, its sign is read back from the lane that holds the winning index.  Lane values are
-// never NaN here (the scan skips NaNs; the NaN-at-position-0 rule is applied after the combine,
-// and a combiner that folds an absorbed NaN overrides its result with it afterwards), so the
-// result is bit-identical to folding Op::comb over the wave.
+// f32 max/min accumulators whose indices are below 2^32 - 1 (tile-relative int32, or absolute
+// int64 in a whole-array reduction of fewer elements) as one unsigned 64-bit key, so that one
+// unsigned max combines two of them instead of Op::comb on (value, index).  The key's high word
+// orders the values (sign-magnitude bits mapped to unsigned order, inverted for min) and is never
+// 0 for a value; its low word is ~index, so among equal values the lowest index wins, and an empty
+// accumulator (key 0) loses to every element.  +0 and -0 compare equal and so share a key (the +0
+// bits): whoever decodes a winning zero restores its sign from the element at the winning index.
+// Accumulator values are never NaN here (the scan skips NaNs; the NaN-at-position-0 rule is
+// applied after the combine), so the result is bit-identical to folding Op::comb.
 template <class Op, class I>
-__device__ inline VI<float, I> wave_reduce_ext_f32(VI<float, I> a) {
-  constexpr bool kMax = Op::kMax;
+__device__ inline uint64_t ext_key_f32(VI<float, I> a) {
   uint32_t u = __builtin_bit_cast(uint32_t, a.val);
   if ((u & 0x7fffffffu) == 0) u = 0;  // -0 -> +0
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  if (!kMax) u = ~u;
-  uint64_t key = a.idx < 0 ? 0 : (uint64_t(u) << 32) | uint32_t(~uint32_t(a.idx));
+  if (!Op::kMax) u = ~u;
+  return a.idx < 0 ? 0 : (uint64_t(u) << 32) | uint32_t(~uint32_t(a.idx));
+}
+// the (value, index) of a key; a zero comes back as +0, and key 0 as the empty accumulator
+template <class Op, class I>
+__device__ inline VI<float, I> ext_unkey_f32(uint64_t key) {
+  if (key == 0) return VI<float, I>{0.0f, I(-1)};
+  uint32_t v = uint32_t(key >> 32);
+  if (!Op::kMax) v = ~v;
+  v = (v & 0x80000000u) ? (v & 0x7fffffffu) : ~v;
+  return VI<float, I>{__builtin_bit_cast(float, v), I(~uint32_t(key))};
+}
+// A whole wave's accumulators combined through their keys (one 64-bit max per butterfly step);
+// a winning zero takes its sign from the lane that holds the winning index.
+template <class Op, class I>
+__device__ inline VI<float, I> wave_reduce_ext_f32(VI<float, I> a) {
+  uint64_t key = ext_key_f32<Op>(a);
 #pragma unroll
   for (int m = kWave / 2; m >= 1; m >>= 1) {
     const uint64_t o = acc_shfl(key, m);
     key = o > key ? o : key;
   }
-  if (key == 0) return VI<float, I>{0.0f, I(-1)};
-  const I idx = I(~uint32_t(key));
-  uint32_t v = uint32_t(key >> 32);
-  if (!kMax) v = ~v;
-  v = (v & 0x80000000u) ? (v & 0x7fffffffu) : ~v;
-  if (v == 0) {  // a zero won (the same key on every lane): take its sign from its lane
-    const bool neg = a.idx == idx && (__builtin_bit_cast(uint32_t, a.val) >> 31);
-    if (__ballot(neg) != 0) v = 0x80000000u;
+  VI<float, I> r = ext_unkey_f32<Op, I>(key);
+  if (key != 0 && __builtin_bit_cast(uint32_t, r.val) == 0) {
+    // a zero won (the same key on every lane): take its sign from its lane
+    const bool neg = a.idx == r.idx && (__builtin_bit_cast(uint32_t, a.val) >> 31);
+    if (__ballot(neg) != 0) r.val = -0.0f;
   }
-  return VI<float, I>{__builtin_bit_cast(float, v), idx};
+  return r;
 }
 
 // Group reduction (GROUP lanes -> lane 0 of the group holds the result).  `idx32`: the caller's
@@ -377,73 +388,89 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
 }
 
 // --------------------------------------------------------------------------------------------
-// Whole-array reduction (one output) on a persistent grid: block b of G streams chunks b, b+G,
-// b+2G, ... (chunk = one round of the block, 512 lanes x UNROLL x 16 bytes), folding each chunk
-// into its lanes' running accumulators in that fixed order; then blocks publish and a combiner
-// block (index G) folds the G block results as in k_reduce_row_fused.  Ordered ops fold a chunk
-// with tile-relative int32 indices and move it into an int64 running accumulator per lane.
+// Whole-array reduction (one output): block b of G streams chunks b, b+G, b+2G, ... (chunk =
+// one round of the block, 512 lanes x UNROLL x 16 bytes; G from launch_reduce_all_fused), folding
+// each chunk into its lanes' running accumulators in that fixed order; then blocks publish and a
+// combiner block (index G) folds the G block results as in k_reduce_row_fused.  Ordered ops fold
+// a chunk with tile-relative int32 indices and move it into an int64 running accumulator per lane.
+//
+// One streaming block's lane accumulator (before the block reduction); `first` receives element 0
+// on lane 0 of the block that reads it.
+template <class OpF, class T, int VEC, int UNROLL>
+__device__ inline typename OpF::A all_stream(const T* __restrict__ a, uint64_t n, uint32_t grid, uint64_t whole_q,
+                                             uint32_t whole_r, uint32_t b, T& first) {
+  using AF = typename OpF::A;
+  constexpr uint64_t kChunk = uint64_t(kRowBS) * UNROLL * VEC;
+  AF acc = OpF::init();
+  // The lane's running accumulator (absolute int64 indices) continues from chunk to chunk, so
+  // an ordered fold searches a chunk only when the chunk beats it.  Whole chunks are software
+  // pipelined: the next chunk's loads are in flight while the current one is folded.
+  constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
+  const uint64_t whole = n / kChunk;
+  uint64_t c = b;
+  Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers: no register copies between chunks
+  auto load = [&](uint64_t cc, Vec<T, VEC>(&dst)[UNROLL]) {
+    const T* p = a + cc * kChunk + threadIdx.x * VEC;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) dst[u] = vload_nt<T, VEC>(p + u * stepk);
+  };
+  auto fold = [&](uint64_t cc, const Vec<T, VEC>(&src)[UNROLL]) {
+    T xs[UNROLL][VEC];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) xs[u][v] = src[u].v[v];
+    if (cc == 0) first = xs[0][0];  // lane 0 holds element 0
+    acc = OpF::template step_chunk<UNROLL, VEC>(acc, xs, threadIdx.x * VEC, stepk, int64_t(cc * kChunk));
+  };
+  // the steady-state loop prefetches unconditionally (a conditional prefetch would make the
+  // wait before each fold cover the prefetch too); the last one or two chunks are peeled.
+  // whole = whole_q * grid + whole_r (from the host: a 64-bit division here would delay every
+  // block's first load)
+  const uint64_t mine = whole_q + (b < whole_r ? 1 : 0);  // whole chunks of this block
+  if (mine > 0) {
+    load(c, x);
+    uint64_t i = 0;
+    for (; i + 2 < mine; i += 2) {
+      load(c + grid, y);
+      fold(c, x);
+      load(c + 2 * grid, x);
+      fold(c + grid, y);
+      c += 2 * grid;
+    }
+    // one or two chunks left.  Written as a conditional load followed by the folds, not as two
+    // branches that both start with fold(c, x): the compiler hoisted that common start above
+    // the branch, so the second chunk's loads waited for the first chunk's data.
+    const bool two = i + 1 < mine;
+    if (two) load(c + grid, y);
+    fold(c, x);
+    if (two) fold(c + grid, y);
+    c = b + mine * grid;  // the first chunk index past this block's whole chunks
+  }
+  if (c == whole && whole * kChunk < n) {  // the last, partial chunk
+    T f{};
+    acc = accumulate_segment<OpF, T, kRowBS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
+                                                          true, f, acc, int64_t(c * kChunk));
+    if (c == 0) first = f;
+  }
+  return acc;
+}
+
+// f32 instances are held to 64 VGPRs (8 waves per SIMD, 4 blocks per CU): the 8-slot combiner
+// would otherwise take them to 68 and a quarter of the resident blocks
+template <class T>
+constexpr int all_fused_waves() { return sizeof(T) == 4 ? 8 : 1; }
 template <class Op, class OpF, class T, int VEC, int UNROLL, int PER>
-__global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict__ a, uint64_t n, uint32_t grid,
-                                                             RedOut<T> out, FusedArgs fa) {
-  using A = typename Op::A;
+__global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fused(const T* __restrict__ a, uint64_t n, uint32_t grid,
+                                                             uint64_t whole_q, uint32_t whole_r, RedOut<T> out,
+                                                             FusedArgs fa) {
   using AF = typename OpF::A;
   static_assert(sizeof(AF) % 4 == 0, "accumulator must split into 32-bit slices");
   constexpr int W = int(sizeof(AF) / 4);
-  constexpr uint64_t kChunk = uint64_t(kRowBS) * UNROLL * VEC;
   const uint32_t b = blockIdx.x;
   if (b < grid) {
-    AF acc = OpF::init();
     T first{};
-    const uint64_t nchunks = (n + kChunk - 1) / kChunk;
-    // The lane's running accumulator (absolute int64 indices) continues from chunk to chunk, so
-    // an ordered fold searches a chunk only when the chunk beats it.  Whole chunks are software
-    // pipelined: the next chunk's loads are in flight while the current one is folded.
-    constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
-    const uint64_t whole = n / kChunk;
-    uint64_t c = b;
-    Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers: no register copies between chunks
-    auto load = [&](uint64_t cc, Vec<T, VEC>(&dst)[UNROLL]) {
-      const T* p = a + cc * kChunk + threadIdx.x * VEC;
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) dst[u] = vload_nt<T, VEC>(p + u * stepk);
-    };
-    auto fold = [&](uint64_t cc, const Vec<T, VEC>(&src)[UNROLL]) {
-      T xs[UNROLL][VEC];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) xs[u][v] = src[u].v[v];
-      if (cc == 0) first = xs[0][0];  // lane 0 holds element 0
-      acc = OpF::template step_chunk<UNROLL, VEC>(acc, xs, threadIdx.x * VEC, stepk, int64_t(cc * kChunk));
-    };
-    // the steady-state loop prefetches unconditionally (a conditional prefetch would make the
-    // wait before each fold cover the prefetch too); the last one or two chunks are peeled
-    const uint64_t mine = c < whole ? (whole - c + grid - 1) / grid : 0;  // whole chunks of this block
-    if (mine > 0) {
-      load(c, x);
-      uint64_t i = 0;
-      for (; i + 2 < mine; i += 2) {
-        load(c + grid, y);
-        fold(c, x);
-        load(c + 2 * grid, x);
-        fold(c + grid, y);
-        c += 2 * grid;
-      }
-      if (i + 1 < mine) {
-        load(c + grid, y);
-        fold(c, x);
-        fold(c + grid, y);
-      } else {
-        fold(c, x);
-      }
-      c = b + mine * grid;  // the first chunk index past this block's whole chunks
-    }
-    if (c == whole && whole * kChunk < n) {  // the last, partial chunk
-      T f{};
-      acc = accumulate_segment<OpF, T, kRowBS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
-                                                            true, f, acc, int64_t(c * kChunk));
-      if (c == 0) first = f;
-    }
+    AF acc = all_stream<OpF, T, VEC, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
     acc = group_reduce<OpF, kRowBS>(acc, n < 0xffffffffull);
     if (threadIdx.x == 0) {
       if (b == 0 && n > 0) acc = absorb_first<OpF, T>(acc, first);
@@ -469,16 +496,93 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_all_fused(const T* __restrict
     __builtin_memcpy(&x, s, sizeof(AF));
     if (bb == 0) first = x;
     r = OpF::comb(r, x);
-#pragma unroll
-    for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
   }
-  if (combiner_gave_up(ok, fa.fault)) return;  // uniform over the block
-  r = group_reduce<OpF, kRowBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
-  if (threadIdx.x == 0) {
-    if constexpr (Op::kOrdered) {
-      if (first.idx == 0 && is_nan(first.val)) r = first;  // block 0 absorbed a NaN at position 0
+  if (!combiner_gave_up(ok, fa.fault)) {  // uniform over the block
+    r = group_reduce<OpF, kRowBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
+    if (threadIdx.x == 0) {
+      if constexpr (Op::kOrdered) {
+        if (first.idx == 0 && is_nan(first.val)) r = first;  // block 0 absorbed a NaN at position 0
+      }
+      write_result<OpF, T, kWriteFinal>(out, 0, r, 0);
     }
-    write_result<OpF, T, kWriteFinal>(out, 0, r, 0);
+  }
+  // The slots go back to zero last: a barrier after these stores would wait for them (on gfx9 a
+  // store holds the vector-memory counter that barriers and later loads wait on until it
+  // reaches memory), which cost 0.7 us per barrier in the combiner of a 64M argmax.
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t bb = threadIdx.x + j * kRowBS;
+    if (bb < grid) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
+    }
+  }
+}
+
+// f32 max / min / argmax / argmin over fewer than 2^32 - 1 elements: the same streaming blocks,
+// each publishing its result as one key (ext_key_f32, two tagged words), so that the combiner
+// folds keys with unsigned maxima.  With the (value, int64 index) accumulator published whole
+// (four words), the combiner's gather and fold took 2.8 us after the last block against 0.8 us
+// for an f32 sum, and its 8-slot version too many registers for the two-chunk grid.  The NaN at
+// position 0 that absorbs the reduction, and the sign of a winning zero, are read back from the
+// input by the combiner.
+template <class Op, class OpF, int UNROLL, int PER>
+__global__ __launch_bounds__(kRowBS, 8) void k_reduce_all_keyed(const float* __restrict__ a, uint64_t n, uint32_t grid,
+                                                                uint64_t whole_q, uint32_t whole_r, RedOut<float> out,
+                                                                FusedArgs fa) {
+  using AF = typename OpF::A;
+  const uint32_t b = blockIdx.x;
+  if (b < grid) {
+    float first = 0.0f;
+    AF acc = all_stream<OpF, float, 4, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
+    acc = group_reduce<OpF, kRowBS>(acc, true);
+    if (threadIdx.x == 0) publish_value<2>(fa.slots + uint64_t(b) * 2, ext_key_f32<OpF>(acc));
+    return;
+  }
+  const float a0 = a[0];  // loaded while the streaming blocks run
+  // the slots in groups of at most 4 per lane (8 at once would spill): blocks are dispatched in
+  // index order, so the earlier group is published first and only the last group's wait is
+  // on the critical path
+  constexpr int kGroup = PER < 4 ? PER : 4;
+  uint64_t key = 0;
+  bool ok = true;
+#pragma clang loop unroll(disable)
+  for (uint32_t base = 0; base < grid; base += kGroup * kRowBS) {
+    uint64_t v[kGroup][2];
+    const uint32_t cnt = grid - base < kGroup * kRowBS ? grid - base : kGroup * kRowBS;
+    ok = gather_published<2, kGroup>(fa.slots + uint64_t(base) * 2, cnt, fa.spin_limit, v) && ok;
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const uint64_t k = (v[j][0] & 0xffffffffu) | (v[j][1] << 32);  // 0 for slots past the grid
+      key = k > key ? k : key;
+    }
+  }
+  if (!combiner_gave_up(ok, fa.fault)) {  // uniform over the block
+#pragma unroll
+    for (int m = kWave / 2; m >= 1; m >>= 1) {
+      const uint64_t o = acc_shfl(key, m);
+      key = o > key ? o : key;
+    }
+    __shared__ uint64_t part[kRowBS / kWave];
+    if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 1; i < kRowBS / kWave; ++i) key = part[i] > key ? part[i] : key;
+      AF r = ext_unkey_f32<OpF, int64_t>(key);
+      if (r.idx >= 0 && r.val == 0.0f) r.val = a[r.idx];  // the first zero's own sign
+      if (is_nan(a0)) r = AF{a0, 0};  // a NaN at position 0 absorbs the whole reduction
+      write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
+    }
+  }
+  // the slots go back to zero after the last barrier, which would otherwise wait for the stores
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t bb = threadIdx.x + j * kRowBS;
+    if (bb < grid) {
+      st_relaxed(fa.slots + uint64_t(bb) * 2, 0);
+      st_relaxed(fa.slots + uint64_t(bb) * 2 + 1, 0);
+    }
   }
 }
 
@@ -919,8 +1023,7 @@ template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c,
 enum : int { kFusedLaunched = 0, kFusedNotCovered = -1, kFusedNoRoom = -2 };
 
 template <class Op, class OpF, class T>
-int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
-                            hipStream_t st);
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, size_t ws_bytes, hipStream_t st);
 
 // The fused single launch for a row-kind reduction split into `tiles` tiles.  kFusedNotCovered
 // (nothing launched) when the shape does not take the 512-lane block path, kFusedNoRoom when the
@@ -942,10 +1045,9 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
   if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return kFusedNotCovered;
   for (int d = 0; d < p.ond; ++d)
     if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return kFusedNotCovered;
-  // one output over one contiguous run: the persistent grid (1024 blocks measured best for 64M
-  // f32: sum 6.5, argmax 6.1 TB/s against 6.1 / 5.9 with one block per tile)
+  // one output over one contiguous run: the interleaved-chunk grid of launch_reduce_all_fused
   if (out_size == 1) {
-    const int r = launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, 1024, ws, ws_bytes, st);
+    const int r = launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, ws, ws_bytes, st);
     if (r != kFusedNotCovered) return r;
   }
   constexpr int V = rvec<T>();
@@ -978,28 +1080,76 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
   return kFusedLaunched;
 }
 
-// whole-array reduction of `n` contiguous, 16-byte aligned elements on a persistent grid of
-// `grid` blocks plus a combiner
+// Whole-array reduction of `n` contiguous, 16-byte aligned elements: G streaming blocks (block b
+// takes chunks b, b + G, ...) plus a combiner.  For accumulators of at most two slot words, G is
+// ceil(chunks / 2), at most kAllMaxBlocks: two 32 KB chunks per block, so that 64M f32 runs four
+// rounds of resident blocks and the dispatcher hands the later blocks to whichever CUs finish
+// first.  Block timestamps of a persistent grid of one round (1024 blocks, 8 chunks each) showed
+// why that matters: blocks with equal work took 9 to 40 us, because their shares of the
+// bandwidth differ, and half the CUs sat idle for the last 30% of the time.  A standalone sweep
+// (64M f32 sum, event-timed over back-to-back launches) gave 43.0 us for the persistent grid
+// against 40.7 us for two chunks per block, 41.8 us for four 16 KB chunks and 43.2-46.7 us for
+// one chunk of 32 or 64 KB per block.  The combiner gathers all of a lane's slots at once, so G
+// is capped by the registers that takes: 4096 blocks for one-word accumulators (f32 sum, prod,
+// mean), 2048 for two words, and the 1024-block grid for wider ones (the ordered ops' value +
+// int64 index, complex sums), whose 8 slots x 4 words would cut the occupancy.
+constexpr uint64_t kAllMaxBlocks = 4096;
 template <class Op, class OpF, class T>
-int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, uint32_t grid, void* ws, size_t ws_bytes,
-                            hipStream_t st) {
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, size_t ws_bytes, hipStream_t st) {
   constexpr int V = rvec<T>();
   constexpr uint64_t kChunk = uint64_t(kRowBS) * 4 * V;
+  constexpr uint64_t W = sizeof(typename OpF::A) / 4;
   if (n == 0 || ws == nullptr || !al16(a)) return kFusedNotCovered;
   const uint64_t nchunks = ceil_div(n, kChunk);
-  if (grid > nchunks) grid = uint32_t(nchunks);
-  if (grid < 2 || grid > 2 * kRowBS) return kFusedNotCovered;
-  const uint64_t W = sizeof(typename OpF::A) / 4;
-  if (uint64_t(grid) * W * 8 > ws_bytes) return kFusedNoRoom;
+  uint64_t grid = W <= 2 ? ceil_div(nchunks, uint64_t(2)) : nchunks;
+  const uint64_t max_grid = W == 1 ? kAllMaxBlocks : W == 2 ? kAllMaxBlocks / 2 : 2 * kRowBS;
+  if (grid > max_grid) grid = max_grid;
+  if (grid < 2) return kFusedNotCovered;
+  if (grid * W * 8 > ws_bytes) return kFusedNoRoom;
   FusedArgs fa{};
   fa.slots = static_cast<uint64_t*>(ws);
   fa.fault = device_fault_word(st);
   fa.spin_limit = wait_spin_limit();
   if (fa.fault == nullptr) return kFusedNotCovered;
-  if (grid <= kRowBS)
-    k_reduce_all_fused<Op, OpF, T, V, 4, 1><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
-  else
-    k_reduce_all_fused<Op, OpF, T, V, 4, 2><<<dim3(grid + 1), kRowBS, 0, st>>>(a, n, grid, out, fa);
+  if constexpr (Op::kOrdered && std::is_same_v<T, float>) {
+    if (n < 0xffffffffull) {  // one key per block, the grid of one-word accumulators
+      uint64_t kg = ceil_div(nchunks, uint64_t(2));
+      if (kg > kAllMaxBlocks) kg = kAllMaxBlocks;
+      if (kg >= 2 && kg * 2 * 8 <= ws_bytes) {
+        const uint32_t g = uint32_t(kg);
+        const uint64_t q = (n / kChunk) / kg;
+        const uint32_t r = uint32_t((n / kChunk) % kg);
+        const dim3 blocks(g + 1);
+        const uint64_t per = ceil_div(kg, uint64_t(kRowBS));
+        if (per == 1)
+          k_reduce_all_keyed<Op, OpF, 4, 1><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+        else if (per == 2)
+          k_reduce_all_keyed<Op, OpF, 4, 2><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+        else if (per <= 4)
+          k_reduce_all_keyed<Op, OpF, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+        else
+          k_reduce_all_keyed<Op, OpF, 4, 8><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+        return kFusedLaunched;
+      }
+    }
+  }
+  const uint32_t g = uint32_t(grid);
+  const dim3 blocks(g + 1);
+  const uint64_t q = (n / kChunk) / grid;
+  const uint32_t r = uint32_t((n / kChunk) % grid);
+  const uint64_t per = ceil_div(grid, uint64_t(kRowBS));
+  if (per == 1) {
+    k_reduce_all_fused<Op, OpF, T, V, 4, 1><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+  } else if (per == 2) {
+    k_reduce_all_fused<Op, OpF, T, V, 4, 2><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+  } else if constexpr (W == 1) {
+    if (per <= 4)
+      k_reduce_all_fused<Op, OpF, T, V, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+    else
+      k_reduce_all_fused<Op, OpF, T, V, 4, 8><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+  } else if constexpr (W == 2) {
+    k_reduce_all_fused<Op, OpF, T, V, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+  }
   return kFusedLaunched;
 }
 
