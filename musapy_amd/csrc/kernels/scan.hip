@@ -7,11 +7,11 @@
 //   look-back  the scanned axis is unit-stride and the rows are few, or each row is one tile: a
 //              single pass with a decoupled look-back (Merrill & Garland, "Single-pass Parallel
 //              Prefix Scan with Decoupled Look-back", 2016) over tiles taken in memory order.
-//   row walk   unit-stride rows that are many (>= 512) and longer than one tile: one block per
-//              row walks it tile by tile, carrying the prefix in registers (no inter-block wait).
-//              Measured faster than the look-back on (1024, 65536) f64 (230 vs 260-290 us): with
-//              that many rows the look-back's round trip per tile costs more than the walk's
-//              one-block-per-row access pattern.
+//   chain      unit-stride rows that are many (>= 512) and longer than one tile: 16 KB tiles in
+//              tile-major order over the rows, each waiting only for its row predecessor's
+//              prefix.  On (1024, 65536) f64: 198 us, against 237 us for one block per row walking
+//              it tile by tile (the previous design, whose one-block-per-row access pattern
+//              topped out at the rate of a plain copy in that pattern) and 205 us for 32 KB tiles.
 //   col        the axis is strided but the innermost other dim is unit-stride: lanes walk
 //              adjacent columns, each carrying a running sum down the axis (coalesced,
 //              sequential order).
@@ -29,13 +29,6 @@ constexpr int kSBlock = 256;
 template <class T> struct ScanAcc { using A = T; };
 template <> struct ScanAcc<int64_t> { using A = uint64_t; };  // wrapping adds
 
-// Shape of the block-per-row kernel: 1024 lanes with one 16-byte vector each (16 KB tiles).  On
-// MI355X a block-per-row stream of (1024, 65536) f64 moved 5.35 TB/s in this shape against 4.82
-// with 256 lanes x 64 bytes and 4.31 with 256 x 128 bytes: many waves with short per-lane
-// tiles hide the per-tile barrier best.  Keeping 2 or 3 tiles of loads in flight instead of 1
-// measured no faster (512- and 1024-lane blocks, 223-328 us against 230 us).
-constexpr int kSeqBlock = 1024;
-template <class T> constexpr int seq_items() { return int(16 / sizeof(T)); }
 
 __device__ inline uint64_t bits_of(double v) { return uint64_t(__double_as_longlong(v)); }
 __device__ inline uint64_t bits_of(float v) { return uint64_t(__float_as_uint(v)); }
@@ -52,21 +45,47 @@ __global__ void k_scan_clear(uint64_t* w, uint64_t n) {
     w[i] = 0;
 }
 
-__device__ inline float shfl_up_acc(float v, int d) { return __shfl_up(v, d, kWave); }
-__device__ inline double shfl_up_acc(double v, int d) { return __shfl_up(v, d, kWave); }
-__device__ inline uint64_t shfl_up_acc(uint64_t v, int d) {
-  return (uint64_t)__shfl_up((unsigned long long)v, d, kWave);
+// Wave-64 inclusive scan with DPP lane moves (gfx9 DPP: row_shr within rows of 16 lanes, then
+// row_bcast:15 / row_bcast:31 across rows).  Against a Hillis-Steele scan over LDS shuffles it
+// makes no LDS round trips, so the scans of several sub-tiles need not be interleaved to hide
+// latency: the look-back kernel went from 111 to 55 VGPRs (f64), from 4 to 8 waves per SIMD.
+// Lanes without a source keep 0; adding +0 changes no value the scan can produce here (every
+// output is formed as +0 + ..., so a -0 input reads back as +0 either way, as in the reference's
+// acc = 0; acc += x).  A fixed association.
+template <int CTRL, int ROW_MASK>
+__device__ inline uint32_t dpp_u32(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, ROW_MASK, 0xf, false));
 }
-
-// wave-64 inclusive scan (Hillis-Steele over shuffles, fixed order)
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ inline float dpp_move(float v) { return __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v))); }
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ inline uint64_t dpp_move(uint64_t v) {
+  return uint64_t(dpp_u32<CTRL, ROW_MASK>(uint32_t(v))) | (uint64_t(dpp_u32<CTRL, ROW_MASK>(uint32_t(v >> 32))) << 32);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ inline double dpp_move(double v) {
+  return __longlong_as_double((long long)dpp_move<CTRL, ROW_MASK>(uint64_t(__double_as_longlong(v))));
+}
 template <class A>
-__device__ inline A wave_incl_scan(A v, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    A u = shfl_up_acc(v, d);
-    if (lane >= d) v = u + v;
-  }
+__device__ inline A wave_incl_scan_dpp(A v) {
+  v = v + dpp_move<0x111>(v);       // row_shr:1
+  v = v + dpp_move<0x112>(v);       // row_shr:2
+  v = v + dpp_move<0x114>(v);       // row_shr:4
+  v = v + dpp_move<0x118>(v);       // row_shr:8
+  v = v + dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = v + dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+template <class A>
+__device__ inline A wave_shr1(A v) { return dpp_move<0x138>(v); }  // wave_shr:1, lane 0 gets 0
+// the value of lane `l` (uniform), through scalar registers
+__device__ inline uint32_t read_lane(uint32_t v, int l) { return uint32_t(__builtin_amdgcn_readlane(int(v), l)); }
+__device__ inline float read_lane(float v, int l) { return __uint_as_float(read_lane(__float_as_uint(v), l)); }
+__device__ inline uint64_t read_lane(uint64_t v, int l) {
+  return uint64_t(read_lane(uint32_t(v), l)) | (uint64_t(read_lane(uint32_t(v >> 32), l)) << 32);
+}
+__device__ inline double read_lane(double v, int l) {
+  return __longlong_as_double((long long)read_lane(uint64_t(__double_as_longlong(v)), l));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -91,6 +110,9 @@ __device__ inline A wave_incl_scan(A v, int lane) {
 // kFaultScanWait, takes P = 0 and still publishes, so every block exits.
 constexpr int kLbBlock = 512;
 constexpr int kVpt = 4;  // 32 KB f64 tiles: measured faster than 16 KB here (fewer look-backs per byte)
+constexpr uint64_t kChainMinRows = 512;  // rows from which the chained scan is used
+constexpr int kChainBlock = 512;
+constexpr int kChainVpt = 2;
 
 struct LbArgs {
   RowIndexer<2> ix;     // non-axis dims: [0] input strides, [1] output strides
@@ -155,24 +177,22 @@ __global__ __launch_bounds__(kLbBlock) void k_scan_lookback(const T* __restrict_
   for (int u = 0; u < kVpt; ++u) {
 #pragma unroll
     for (int e = 1; e < VE; ++e) x[u][e] = x[u][e - 1] + x[u][e];
-    incl[u] = wave_incl_scan(x[u][VE - 1], lane);
+    incl[u] = wave_incl_scan_dpp(x[u][VE - 1]);
     if (lane == kWave - 1) s_wave[u][wv] = incl[u];
+    incl[u] = wave_shr1(incl[u]);  // from here on: the lane's exclusive offset in its wave
   }
   __syncthreads();
-  // exclusive offset of each lane's run inside the tile, and the tile aggregate (fixed order)
+  // exclusive offset of each lane's run inside the tile, and the tile aggregate (fixed order):
+  // lanes 0 .. kWaves-1 read the sub-tile's wave totals and scan them, and every lane takes its
+  // wave's exclusive offset and the sub-tile total from that scan (one LDS read per lane)
   A lane_off[kVpt];
   A run = A(0);
 #pragma unroll
   for (int u = 0; u < kVpt; ++u) {
-    A wo = A(0), st = A(0);
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-      if (i < wv) wo = wo + s_wave[u][i];
-      st = st + s_wave[u][i];
-    }
-    A le = shfl_up_acc(incl[u], 1);
-    if (lane == 0) le = A(0);
-    lane_off[u] = run + (wo + le);
+    const A ws = wave_incl_scan_dpp(lane < kWaves ? s_wave[u][lane] : A(0));
+    const A st = read_lane(ws, kWaves - 1);
+    const A wo = wv > 0 ? read_lane(ws, wv - 1) : A(0);
+    lane_off[u] = run + (wo + incl[u]);
     run = run + st;
   }
   const A agg = run;
@@ -252,79 +272,150 @@ __global__ __launch_bounds__(kLbBlock) void k_scan_lookback(const T* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// Row walk, for many rows: block b walks row b tile by tile, keeping the running prefix P in
-// registers and prefetching the next tile while it scans the current one.  The association is
-// fixed by the shape (lane, wave, tile), so results are identical run to run.
-struct RowScanArgs {
+// Chained row scan, for many rows of several tiles: tile t of row r is block t * R8 + r (R8 =
+// rows rounded up to a multiple of 8, the blocks past the last row exit at once), so the grid
+// streams tile 0 of every row, then tile 1 of every row, ...  The tile layout and in-tile scan are
+// k_scan_lookback's, with kChainBlock lanes x kChainVpt vectors per tile; a tile's prefix is
+// always P(t) = P(t - 1) + A(t), a fixed association.  Block (r, t) waits only for P(r, t - 1),
+// published by block (r, t - 1): R8 blocks earlier, and on the same XCD (blocks go to the 8 XCDs
+// round-robin by index, and R8 is a multiple of 8), whose workgroups are dispatched in index
+// order -- so the block it waits on is resident or finished, and no atomic tile counter is
+// needed.  The predecessor's prefix is read together with the tile's own loads, and a timing copy
+// that skipped the wait ran as fast: the chain costs nothing measurable at C5, and so does the
+// in-tile scan (a copy in the same block shape took as long).  The tile shape sets the rate:
+// 512 x 2 vectors 198 us, 512 x 4 205 us, 512 x 1 206 us, 256 x 4 215 us, 256 x 2 249 us
+// ((1024, 65536) f64; the smaller tiles lengthen the per-row chain).  A wait is bounded
+// (wait_spin_limit polls): when it runs out the tile records kFaultScanWait, takes P = 0 and
+// still publishes, so every block exits.
+struct ChainArgs {
   RowIndexer<2> ix;     // non-axis dims: [0] input strides, [1] output strides
   uint64_t L;
+  FastDiv rdiv;         // divides a block id by R8
+  uint32_t R8;          // rows rounded up to a multiple of 8
+  uint32_t rows;
   uint32_t tiles;       // tiles per row
+  uint64_t* prefix;     // per (row, tile): W words of P(row, tile)
+  uint32_t* fault;      // the device's fault word (kcommon.hpp)
+  uint32_t spin_limit;  // polls a wait may make
   bool vec;             // 16-byte aligned rows
+  bool nt_load, nt_store;
 };
 
-template <class T>
-__device__ inline void load_tile(const T* ain, uint64_t k0, uint64_t L, bool vec,
-                                 typename ScanAcc<T>::A (&x)[seq_items<T>()]) {
+template <class T, int BS, int VPT>
+__global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* __restrict__ c, ChainArgs sa) {
   using A = typename ScanAcc<T>::A;
-  constexpr int N = seq_items<T>();
-  if (vec && k0 + N <= L) {
-    Vec<T, N> v = vload<T, N>(ain + k0);
-#pragma unroll
-    for (int q = 0; q < N; ++q) x[q] = A(v.v[q]);
-  } else {
-#pragma unroll
-    for (int j = 0; j < N; ++j) x[j] = (k0 + j < L) ? A(ain[k0 + j]) : A(0);
-  }
-}
-
-template <class T>
-__global__ __launch_bounds__(kSeqBlock) void k_scan_rows_seq(const T* __restrict__ a, T* __restrict__ c,
-                                                             RowScanArgs sa) {
-  using A = typename ScanAcc<T>::A;
-  constexpr int N = seq_items<T>();
-  constexpr uint64_t TILE = uint64_t(kSeqBlock) * N;
-  constexpr int kWaves = kSeqBlock / kWave;
-  __shared__ A s_wave[2][kWaves];
+  constexpr int VE = int(16 / sizeof(T));
+  constexpr int kWaves = BS / kWave;
+  constexpr uint64_t TE = uint64_t(BS) * VPT * VE;
+  constexpr int W = sizeof(A) == 4 ? 1 : 2;
+  __shared__ A s_wave[VPT][kWaves];
+  __shared__ A s_prefix;
   const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
-  const uint32_t row = blockIdx.x;
+  const uint32_t chunk = fd_div(sa.rdiv, blockIdx.x);
+  const uint32_t row = blockIdx.x - chunk * sa.R8;
+  if (row >= sa.rows) return;
   int64_t off[2];
   row_offsets<2>(sa.ix, row, off);
   const T* ain = a + off[0];
   T* cout = c + off[1];
-  A x[N], y[N];
-  load_tile<T>(ain, uint64_t(tid) * N, sa.L, sa.vec, x);
-  A P = A(0);
-  for (uint32_t t = 0; t < sa.tiles; ++t) {
-    const uint64_t k0 = uint64_t(t) * TILE + uint64_t(tid) * N;
-    if (t + 1 < sa.tiles) load_tile<T>(ain, k0 + TILE, sa.L, sa.vec, y);
+  const uint64_t t0 = uint64_t(chunk) * TE;
+  const bool full = sa.vec && t0 + TE <= sa.L;
+
+  A x[VPT][VE];
+  if (full) {
+    Vec<T, VE> v[VPT];
 #pragma unroll
-    for (int j = 1; j < N; ++j) x[j] = x[j - 1] + x[j];
-    A tot = x[N - 1];
-    A incl = wave_incl_scan(tot, lane);
-    if (lane == kWave - 1) s_wave[t & 1][wv] = incl;  // double-buffered: no barrier needed after use
-    __syncthreads();
-    A wave_off = A(0), agg = A(0);
+    for (int u = 0; u < VPT; ++u) v[u] = vload_pol<T, VE>(ain + t0 + (uint64_t(u) * BS + tid) * VE, sa.nt_load);
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-      if (i < wv) wave_off = wave_off + s_wave[t & 1][i];
-      agg = agg + s_wave[t & 1][i];
+    for (int u = 0; u < VPT; ++u)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) x[u][e] = A(v[u].v[e]);
+  } else {
+#pragma unroll
+    for (int u = 0; u < VPT; ++u)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const uint64_t k = t0 + (uint64_t(u) * BS + tid) * VE + e;
+        x[u][e] = k < sa.L ? A(ain[k]) : A(0);
+      }
+  }
+  // the predecessor's prefix is read now, so that this round trip overlaps the tile's loads
+  // instead of following the in-tile scan (it is usually published by then)
+  uint64_t* const rowp = sa.prefix + uint64_t(row) * sa.tiles * W;
+  uint64_t pw[W];
+#pragma unroll
+  for (int q = 0; q < W; ++q) pw[q] = 0;
+  if (tid == 0 && chunk > 0) {
+#pragma unroll
+    for (int q = 0; q < W; ++q) pw[q] = ld_relaxed(rowp + uint64_t(chunk - 1) * W + q);
+  }
+  // in-lane inclusive runs, then a wave scan of the run totals per sub-tile
+  A incl[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+#pragma unroll
+    for (int e = 1; e < VE; ++e) x[u][e] = x[u][e - 1] + x[u][e];
+    incl[u] = wave_incl_scan_dpp(x[u][VE - 1]);
+    if (lane == kWave - 1) s_wave[u][wv] = incl[u];
+    incl[u] = wave_shr1(incl[u]);  // from here on: the lane's exclusive offset in its wave
+  }
+  __syncthreads();
+  // exclusive offset of each lane's run inside the tile, and the tile aggregate (fixed order):
+  // lanes 0 .. kWaves-1 read the sub-tile's wave totals and scan them, and every lane takes its
+  // wave's exclusive offset and the sub-tile total from that scan (one LDS read per lane)
+  A lane_off[VPT];
+  A run = A(0);
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const A ws = wave_incl_scan_dpp(lane < kWaves ? s_wave[u][lane] : A(0));
+    const A st = read_lane(ws, kWaves - 1);
+    const A wo = wv > 0 ? read_lane(ws, wv - 1) : A(0);
+    lane_off[u] = run + (wo + incl[u]);
+    run = run + st;
+  }
+  const A agg = run;
+
+  if (tid == 0) {
+    A P = A(0);
+    if (chunk > 0) {
+      bool got = sa.spin_limit > 0;  // a limit of 0 gives up before the first poll
+      uint64_t bits = 0;
+#pragma unroll
+      for (int q = 0; q < W; ++q) {
+        got = got && (pw[q] & kTag);
+        bits |= (pw[q] & 0xffffffffu) << (32 * q);
+      }
+      for (uint32_t spins = 1; !got && spins < sa.spin_limit; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        got = read_value<W>(rowp + uint64_t(chunk - 1) * W, bits);
+      }
+      if (got)
+        P = from_bits<A>(bits);
+      else
+        atomicOr(sa.fault, kFaultScanWait);  // the prefix stays 0
     }
-    A lane_excl = shfl_up_acc(incl, 1);
-    if (lane == 0) lane_excl = A(0);
-    const A local = wave_off + lane_excl;
-    if (sa.vec && k0 + N <= sa.L) {
-      Vec<T, N> v;
+    if (chunk + 1 < sa.tiles) publish_value<W>(rowp + uint64_t(chunk) * W, bits_of(A(P + agg)));
+    s_prefix = P;
+  }
+  __syncthreads();
+  const A P = s_prefix;
+
+  if (full) {
 #pragma unroll
-      for (int q = 0; q < N; ++q) v.v[q] = T(P + (local + x[q]));
-      vstore<T, N>(cout + k0, v);
-    } else {
+    for (int u = 0; u < VPT; ++u) {
+      Vec<T, VE> v;
 #pragma unroll
-      for (int j = 0; j < N; ++j)
-        if (k0 + j < sa.L) cout[k0 + j] = T(P + (local + x[j]));
+      for (int e = 0; e < VE; ++e) v.v[e] = T(P + (lane_off[u] + x[u][e]));
+      vstore_pol<T, VE>(cout + t0 + (uint64_t(u) * BS + tid) * VE, v, sa.nt_store);
     }
-    P = P + agg;
+  } else {
 #pragma unroll
-    for (int j = 0; j < N; ++j) x[j] = y[j];
+    for (int u = 0; u < VPT; ++u)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const uint64_t k = t0 + (uint64_t(u) * BS + tid) * VE + e;
+        if (k < sa.L) cout[k] = T(P + (lane_off[u] + x[u][e]));
+      }
   }
 }
 
@@ -394,15 +485,45 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
       if (((p.istride[d] * int64_t(sizeof(T))) % 16) || ((p.ostride[d] * int64_t(sizeof(T))) % 16)) vec = false;
     constexpr uint64_t TE = uint64_t(kLbBlock) * kVpt * (16 / sizeof(T));
     const uint64_t tiles = (p.L + TE - 1) / TE;
-    // many rows of several tiles: walk each row in one block, no look-back
-    if (tiles > 1 && p.rows >= 512) {
-      RowScanArgs ss{};
-      ss.ix = ix;
-      ss.L = p.L;
-      ss.vec = vec;
-      constexpr uint64_t STILE = uint64_t(kSeqBlock) * seq_items<T>();
-      ss.tiles = uint32_t((p.L + STILE - 1) / STILE);
-      k_scan_rows_seq<T><<<dim3(unsigned(p.rows)), kSeqBlock, 0, st>>>(a, c, ss);
+    // many rows of several tiles: the chained scan, tile-major over the rows
+    constexpr uint64_t CTE = uint64_t(kChainBlock) * kChainVpt * (16 / sizeof(T));
+    const uint64_t ctiles = (p.L + CTE - 1) / CTE;
+    if (ctiles > 1 && p.rows >= kChainMinRows) {
+      const uint64_t tiles = ctiles;
+      const uint64_t R8 = (uint64_t(p.rows) + 7) / 8 * 8;
+      if (R8 * tiles >= (uint64_t(1) << 31)) {  // block ids
+        g_wrapper_error = 4;
+        return;
+      }
+      const uint64_t bpr = (p.L + 255) / 256;
+      const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
+      const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
+      const uint64_t words = uint64_t(p.rows) * tiles * W;
+      if (tmp == nullptr || words * 8 > cap) {
+        g_wrapper_error = 1;
+        return;
+      }
+      ChainArgs ca{};
+      ca.ix = ix;
+      ca.L = p.L;
+      ca.R8 = uint32_t(R8);
+      ca.rdiv = make_fastdiv(ca.R8);
+      ca.rows = uint32_t(p.rows);
+      ca.tiles = uint32_t(tiles);
+      ca.prefix = reinterpret_cast<uint64_t*>(tmp);
+      ca.fault = device_fault_word(st);
+      ca.spin_limit = wait_spin_limit();
+      ca.vec = vec;
+      const uint64_t bytes = uint64_t(p.rows) * p.L * sizeof(T);
+      ca.nt_load = bytes >= kStreamLoadBytes;
+      ca.nt_store = bytes >= kStreamStoreBytes;
+      if (ca.fault == nullptr) {
+        g_wrapper_error = 1;
+        return;
+      }
+      unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
+      k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
+      k_scan_chain<T, kChainBlock, kChainVpt><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
       return;
     }
     if (uint64_t(p.rows) * tiles >= (uint64_t(1) << 32)) {  // tile ids are 32-bit

@@ -354,12 +354,12 @@ def test_cumsum_deterministic():
     s = ms.sum(X, axis=1).numpy()
     for _ in range(3):
         assert_bits_equal(ms.sum(X, axis=1).numpy(), s, "sum run-to-run")
-    # many rows: the block-per-row scan (no look-back)
+    # many rows: the chained scan (tile-major over the rows, each tile waits for its predecessor)
     y = RNG.random((600, 40000))
     Y = dev(y)
     b = ms.cumsum(Y, axis=1).numpy()
     for _ in range(2):
-        assert_bits_equal(ms.cumsum(Y, axis=1).numpy(), b, "row-per-block cumsum run-to-run")
+        assert_bits_equal(ms.cumsum(Y, axis=1).numpy(), b, "chained cumsum run-to-run")
     want = R.cumsum(y[:4], 1)
     assert np.all(np.abs(b[:4] - want) <= 1e-12 * np.abs(want))
 
@@ -457,3 +457,32 @@ def test_whole_array_signed_zero_ties(kind):
     idx = RNG.choice(np.arange(1_000_000, n), 5000, replace=False)
     x[idx] = np.where(RNG.random(5000) < 0.5, -0.0, 0.0).astype(np.float32)
     check_reduce(kind, x, None)
+
+
+def test_cumsum_chained_rows():
+    """Many rows of several tiles take the chained scan: row counts that are not a multiple of 8
+    (the grid pads the row pitch to one), ragged last tiles, rows that are not 16-byte aligned
+    (a sliced view), int64 exact, floats within the prefix bound of the oracle, and the same bits
+    on every run."""
+    cases = [((515, 70001), np.float64), ((777, 20000), np.int64), ((513, 33333), np.float32),
+             ((600, 4097), np.float64), ((1030, 8192), np.float32)]
+    for shape, dt in cases:
+        x = RNG.integers(-1000, 1000, shape) if dt == np.int64 else RNG.random(shape)
+        x = x.astype(dt)
+        X = dev(x)
+        got = ms.cumsum(X, axis=1).numpy()
+        want = R.cumsum(x, 1)
+        what = f"chained cumsum {np.dtype(dt).name} {shape}"
+        if dt == np.int64:
+            assert_bits_equal(got, want, what)
+        else:
+            exact = np.cumsum(x.astype(np.float64), axis=1)
+            bound = TOL[dt] * np.cumsum(np.abs(x.astype(np.float64)), axis=1) + np.abs(want - exact)
+            assert np.all(np.abs(got - want) <= bound), what
+        assert_bits_equal(ms.cumsum(X, axis=1).numpy(), got, what + " run-to-run")
+    # a view whose rows start 8 bytes past 16-byte alignment: the element-wise load path
+    base = RNG.random((520, 9001))
+    V = ms.slice(dev(base), [(0, 520, 1), (1, 9001, 1)])
+    got = ms.cumsum(V, axis=1).numpy()
+    want = R.cumsum(base[:, 1:], 1)
+    assert np.all(np.abs(got - want) <= 1e-12 * np.cumsum(np.abs(base[:, 1:]), axis=1)), "unaligned chained rows"

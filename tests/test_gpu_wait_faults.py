@@ -97,6 +97,16 @@ def test_row_scan_look_back_gives_up_and_recovers():
     _fresh_stream_case(lambda: (ms.from_numpy(y),), lambda Y: ms.cumsum(Y, axis=1), check)
 
 
+def test_chained_row_scan_gives_up_and_recovers():
+    y = RNG.random((520, 20_000))
+    want = R.cumsum(y, 1)
+
+    def check(got, what):
+        assert np.all(np.abs(got - want) <= 1e-12 * np.cumsum(np.abs(y), axis=1)), what
+
+    _fresh_stream_case(lambda: (ms.from_numpy(y),), lambda Y: ms.cumsum(Y, axis=1), check)
+
+
 def test_c_abi_fault_word_and_workspace_reuse():
     """A caller of musapy_reduce_fused_v1 reads the fault with musapy_kernels_take_fault after its
     synchronize, zeroes its workspace, and the next call is correct."""
