@@ -324,6 +324,18 @@ enum { MUSAPY_RED_SUM = 0, MUSAPY_RED_PROD, MUSAPY_RED_MAX, MUSAPY_RED_MIN, MUSA
        MUSAPY_RED_ARGMIN };
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---- cumsum on a zeroed workspace (new; no counterpart in kernels.rs) ----
+ * The chained scan of musapy_cumsum_*_v3 for many (>= 512) unit-stride rows of several tiles,
+ * with its per-tile prefixes in `workspace` instead of the reference's scratch `tmp`: the
+ * workspace must be zero before the call and is left zero (each prefix is returned to zero by
+ * the tile that reads it), so no clearing launch is needed.  Needs rows * tiles * W 64-bit words
+ * (W = 1 for f32, 2 for f64/i64; a tile is 2048 f32 or 1024 f64/i64 elements).  `dtype` is
+ * MUSAPY_DT_I64, _F32 or _F64.  Returns 0 when launched, -1 when the call does not take that path
+ * or the workspace is too small (nothing launched: use musapy_cumsum_*_v3).  Calls that share a
+ * workspace must be ordered; after a device wait fault (musapy_kernels_take_fault) zero it
+ * again. */
+int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---- max / min over both axes of a 2-D array in one launch (new; no counterpart in kernels.rs) ----
  * `a` is a C-contiguous (rows, cols) array of the compute dtype (F32, F64 or I64), and `c`
  * receives one value.  The result is bit for bit what the reference's per-axis

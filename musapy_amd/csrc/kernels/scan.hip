@@ -389,10 +389,15 @@ __global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* _
         __builtin_amdgcn_s_sleep(1);
         got = read_value<W>(rowp + uint64_t(chunk - 1) * W, bits);
       }
-      if (got)
+      if (got) {
         P = from_bits<A>(bits);
-      else
+        // nothing else reads the predecessor's prefix: return its words to zero, so that the
+        // launch leaves the prefix area as it found it (the last tile of a row publishes nothing)
+#pragma unroll
+        for (int q = 0; q < W; ++q) st_relaxed(rowp + uint64_t(chunk - 1) * W + q, 0);
+      } else {
         atomicOr(sa.fault, kFaultScanWait);  // the prefix stays 0
+      }
     }
     if (chunk + 1 < sa.tiles) publish_value<W>(rowp + uint64_t(chunk) * W, bits_of(A(P + agg)));
     s_prefix = P;
@@ -455,12 +460,21 @@ __global__ __launch_bounds__(kSBlock) void k_scan_seq(const T* __restrict__ a, T
 
 // ---------------------------------------------------------------------------------------------
 
-template <class T>
-void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
-                   size_t axis_len, size_t out_size, hipStream_t st) {
-  if (out_size == 0 || axis_len == 0) return;
-  if (!args_ok(ndim, axis)) return;
+// What a cumsum call resolves to, shared by the reference-signature entry points (scratch
+// `tmp` of the reference's size, arbitrary contents) and musapy_cumsum_ws_v1 (a zeroed workspace).
+struct ScanShape {
   ScanPlan p;
+  RowIndexer<2> ix;  // non-axis dims, innermost first (row scans)
+  bool vec = false;  // 16-byte aligned rows
+};
+
+// Plans the call; false (with the wrapper error set when it is one) when nothing is to be done.
+template <class T>
+bool plan_cumsum(ScanShape& sh, const T* a, const T* c, int ndim, const size_t* shape, const ssize_t* strides,
+                 int axis, size_t axis_len, size_t out_size) {
+  if (out_size == 0 || axis_len == 0) return false;
+  if (!args_ok(ndim, axis)) return false;
+  ScanPlan& p = sh.p;
   plan_scan(p, ndim, shape, strides, axis);
   // rows and the non-axis extents are decoded in 32 bits (row_offsets, the lane index of
   // k_scan_seq): refuse shapes past that instead of aliasing rows
@@ -468,80 +482,106 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
   for (int d = 0; d < p.ond; ++d) fits = fits && p.oshape[d] < (uint64_t(1) << 32);
   if (!fits) {
     g_wrapper_error = 4;
-    return;
+    return false;
   }
-  if (p.kind == kRowScan && p.L > 16) {
-    RowIndexer<2> ix{};  // non-axis dims, innermost first
-    ix.nd = p.ond;
+  if (p.kind == kRowScan) {
+    sh.ix = RowIndexer<2>{};
+    sh.ix.nd = p.ond;
     for (int i = 0; i < p.ond; ++i) {
       int d = p.ond - 1 - i;
-      ix.div[i] = make_fastdiv(uint32_t(p.oshape[d]));
-      ix.stride[0][i] = p.istride[d];
-      ix.stride[1][i] = p.ostride[d];
+      sh.ix.div[i] = make_fastdiv(uint32_t(p.oshape[d]));
+      sh.ix.stride[0][i] = p.istride[d];
+      sh.ix.stride[1][i] = p.ostride[d];
     }
-    if (p.ond == 1 && p.oshape[0] == 1) ix.nd = 0;
-    bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c)) & 15u) == 0;
+    if (p.ond == 1 && p.oshape[0] == 1) sh.ix.nd = 0;
+    sh.vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c)) & 15u) == 0;
     for (int d = 0; d < p.ond; ++d)
-      if (((p.istride[d] * int64_t(sizeof(T))) % 16) || ((p.ostride[d] * int64_t(sizeof(T))) % 16)) vec = false;
-    constexpr uint64_t TE = uint64_t(kLbBlock) * kVpt * (16 / sizeof(T));
-    const uint64_t tiles = (p.L + TE - 1) / TE;
+      if (((p.istride[d] * int64_t(sizeof(T))) % 16) || ((p.ostride[d] * int64_t(sizeof(T))) % 16)) sh.vec = false;
+  }
+  return true;
+}
+
+// tiles of the chained scan per row, 0 when the call does not take it
+template <class T>
+uint64_t chain_tiles(const ScanShape& sh) {
+  constexpr uint64_t CTE = uint64_t(kChainBlock) * kChainVpt * (16 / sizeof(T));
+  if (sh.p.kind != kRowScan || sh.p.L <= 16 || sh.p.rows < kChainMinRows) return 0;
+  const uint64_t tiles = (sh.p.L + CTE - 1) / CTE;
+  return tiles > 1 ? tiles : 0;
+}
+
+// The chained scan over `prefix` (rows * tiles * W words).  With `clear` the words are zeroed
+// first; without, they must be zero already (the launch leaves them zero).
+template <class T>
+void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_t* prefix, bool clear,
+                  hipStream_t st) {
+  const ScanPlan& p = sh.p;
+  const uint64_t R8 = (uint64_t(p.rows) + 7) / 8 * 8;
+  if (R8 * tiles >= (uint64_t(1) << 31)) {  // block ids
+    g_wrapper_error = 4;
+    return;
+  }
+  const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
+  const uint64_t words = uint64_t(p.rows) * tiles * W;
+  ChainArgs ca{};
+  ca.ix = sh.ix;
+  ca.L = p.L;
+  ca.R8 = uint32_t(R8);
+  ca.rdiv = make_fastdiv(ca.R8);
+  ca.rows = uint32_t(p.rows);
+  ca.tiles = uint32_t(tiles);
+  ca.prefix = prefix;
+  ca.fault = device_fault_word(st);
+  ca.spin_limit = wait_spin_limit();
+  ca.vec = sh.vec;
+  const uint64_t bytes = uint64_t(p.rows) * p.L * sizeof(T);
+  ca.nt_load = bytes >= kStreamLoadBytes;
+  ca.nt_store = bytes >= kStreamStoreBytes;
+  if (ca.fault == nullptr) {  // a wait that ran out could not be reported: take no waits
+    g_wrapper_error = 1;
+    return;
+  }
+  if (clear) {
+    unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
+    k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
+  }
+  k_scan_chain<T, kChainBlock, kChainVpt><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
+}
+
+template <class T>
+void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                   size_t axis_len, size_t out_size, hipStream_t st) {
+  ScanShape sh;
+  if (!plan_cumsum<T>(sh, a, c, ndim, shape, strides, axis, axis_len, out_size)) return;
+  const ScanPlan& p = sh.p;
+  // tmp capacity per the caller's formula: rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
+  const uint64_t bpr = (p.L + 255) / 256;
+  const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
+  const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
+  if (p.kind == kRowScan && p.L > 16) {
     // many rows of several tiles: the chained scan, tile-major over the rows
-    constexpr uint64_t CTE = uint64_t(kChainBlock) * kChainVpt * (16 / sizeof(T));
-    const uint64_t ctiles = (p.L + CTE - 1) / CTE;
-    if (ctiles > 1 && p.rows >= kChainMinRows) {
-      const uint64_t tiles = ctiles;
-      const uint64_t R8 = (uint64_t(p.rows) + 7) / 8 * 8;
-      if (R8 * tiles >= (uint64_t(1) << 31)) {  // block ids
-        g_wrapper_error = 4;
-        return;
-      }
-      const uint64_t bpr = (p.L + 255) / 256;
-      const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
-      const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
-      const uint64_t words = uint64_t(p.rows) * tiles * W;
-      if (tmp == nullptr || words * 8 > cap) {
+    if (const uint64_t ct = chain_tiles<T>(sh)) {
+      if (tmp == nullptr || uint64_t(p.rows) * ct * W * 8 > cap) {
         g_wrapper_error = 1;
         return;
       }
-      ChainArgs ca{};
-      ca.ix = ix;
-      ca.L = p.L;
-      ca.R8 = uint32_t(R8);
-      ca.rdiv = make_fastdiv(ca.R8);
-      ca.rows = uint32_t(p.rows);
-      ca.tiles = uint32_t(tiles);
-      ca.prefix = reinterpret_cast<uint64_t*>(tmp);
-      ca.fault = device_fault_word(st);
-      ca.spin_limit = wait_spin_limit();
-      ca.vec = vec;
-      const uint64_t bytes = uint64_t(p.rows) * p.L * sizeof(T);
-      ca.nt_load = bytes >= kStreamLoadBytes;
-      ca.nt_store = bytes >= kStreamStoreBytes;
-      if (ca.fault == nullptr) {
-        g_wrapper_error = 1;
-        return;
-      }
-      unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
-      k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
-      k_scan_chain<T, kChainBlock, kChainVpt><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
+      launch_chain<T>(a, c, sh, ct, reinterpret_cast<uint64_t*>(tmp), true, st);
       return;
     }
+    constexpr uint64_t TE = uint64_t(kLbBlock) * kVpt * (16 / sizeof(T));
+    const uint64_t tiles = (p.L + TE - 1) / TE;
     if (uint64_t(p.rows) * tiles >= (uint64_t(1) << 32)) {  // tile ids are 32-bit
       g_wrapper_error = 4;
       return;
     }
     LbArgs sa{};
-    sa.ix = ix;
+    sa.ix = sh.ix;
     sa.L = p.L;
-    sa.vec = vec;
+    sa.vec = sh.vec;
     sa.tiles = uint32_t(tiles);
     sa.tdiv = make_fastdiv(sa.tiles);
     if (tiles > 1) {
-      // tmp capacity per the caller's formula: rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
-      const uint64_t bpr = (p.L + 255) / 256;
-      const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
       // word 0: the tile claim counter; then 2 * W status words per tile (aggregate, prefix)
-      const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
       const uint64_t words = 1 + uint64_t(p.rows) * tiles * 2 * W;
       if (tmp == nullptr || words * 8 > cap) {
         g_wrapper_error = 1;
@@ -578,6 +618,20 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
   k_scan_seq<T><<<grid, kSBlock, 0, st>>>(a, c, sq);
 }
 
+// musapy_cumsum_ws_v1: the chained scan on a zeroed workspace, or kFusedNotCovered-style -1
+template <class T>
+int launch_cumsum_ws(const T* a, T* c, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                     size_t axis_len, size_t out_size, void* ws, size_t ws_bytes, hipStream_t st) {
+  ScanShape sh;
+  if (ws == nullptr || out_size == 0 || axis_len == 0 || !args_ok(ndim, axis)) return -1;
+  if (!plan_cumsum<T>(sh, a, c, ndim, shape, strides, axis, axis_len, out_size)) return -1;
+  const uint64_t ct = chain_tiles<T>(sh);
+  const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
+  if (ct == 0 || uint64_t(sh.p.rows) * ct * W * 8 > ws_bytes) return -1;
+  launch_chain<T>(a, c, sh, ct, static_cast<uint64_t*>(ws), false, st);
+  return 0;
+}
+
 }  // namespace mpy
 
 using namespace mpy;
@@ -596,6 +650,27 @@ void musapy_cumsum_f32_v3(const float* a, float* c, float* tmp, int ndim, const 
 void musapy_cumsum_f64_v3(const double* a, double* c, double* tmp, int ndim, const size_t* in_shape,
                           const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t st) {
   launch_cumsum<double>(a, c, tmp, ndim, in_shape, in_strides, axis, axis_len, out_size, st);
+}
+
+// The chained scan with a zeroed workspace instead of the reference's scratch (new; no
+// counterpart in kernels.rs): 0 when launched, -1 when the call does not take the chained path
+// or the workspace is too small (nothing launched; use musapy_cumsum_*_v3).
+int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
+                        const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, void* workspace,
+                        size_t workspace_bytes, hipStream_t st) {
+  switch (dtype) {
+    case MUSAPY_DT_I64:
+      return launch_cumsum_ws<int64_t>(static_cast<const int64_t*>(a), static_cast<int64_t*>(c), ndim, in_shape,
+                                       in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
+    case MUSAPY_DT_F32:
+      return launch_cumsum_ws<float>(static_cast<const float*>(a), static_cast<float*>(c), ndim, in_shape,
+                                     in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
+    case MUSAPY_DT_F64:
+      return launch_cumsum_ws<double>(static_cast<const double*>(a), static_cast<double*>(c), ndim, in_shape,
+                                      in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
+    default:
+      return -1;
+  }
 }
 
 // Returns and clears the calling thread's last wrapper-level error (1 = cumsum scratch missing

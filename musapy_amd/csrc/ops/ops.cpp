@@ -843,12 +843,21 @@ Array cumsum_op(const Array& a, std::optional<size_t> axis, const Array* out) {
       throw ShapeError("cumsum: axis_len " + std::to_string(axis_len) +
                        " exceeds max supported length 16777216 (256^3)");
     const size_t rows = out_size / std::max<size_t>(axis_len, 1);
+    const int nd = int(kshape.size());
+    s->note_bounded_wait();  // row scans split into tiles wait on their predecessors
+    // many rows: the chained scan on the stream's zeroed workspace (no scratch, no clear launch)
+    const int dt = ct == Dtype::Int64 ? MUSAPY_DT_I64 : ct == Dtype::Float32 ? MUSAPY_DT_F32 : MUSAPY_DT_F64;
+    if (musapy_cumsum_ws_v1(dt, aw->data_ptr(), r.data_ptr(), nd, kshape.data(), kstrides.data(), kaxis, axis_len,
+                            out_size, s->reduce_workspace(), Stream::kReduceWorkspaceBytes, s->raw()) == 0) {
+      check_launch("cumsum");
+      aw->data->record_read(s);
+      r.data->record_write(s);
+      return r;
+    }
     const size_t scratch = bpr > 256 ? rows * (bpr + (bpr + 255) / 256) : rows * bpr;
     BufferRef tmp;
     if (bpr > 1) tmp = Buffer::alloc(scratch * element_size(ct), a.device, s);
     void* tp = tmp ? tmp->ptr() : nullptr;
-    const int nd = int(kshape.size());
-    s->note_bounded_wait();  // row scans split into tiles wait on their predecessors
     if (ct == Dtype::Int64)
       musapy_cumsum_i64_v3((const int64_t*)aw->data_ptr(), (int64_t*)r.data_ptr(), (int64_t*)tp, nd, kshape.data(),
                            kstrides.data(), kaxis, axis_len, out_size, s->raw());

@@ -342,3 +342,53 @@ def test_cumsum_with_reference_scratch(dt):
                 # matches it exactly; a tiled row scan is held to the exact sums).
                 bound = bound + np.abs(want - np.cumsum(view.astype(np.float64), axis=ax))
             assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-30), what
+
+
+@pytest.mark.parametrize("dt", [np.int64, np.float32, np.float64])
+def test_cumsum_workspace_entry_matches_scratch_entry(dt):
+    """musapy_cumsum_ws_v1 (new; the chained scan on a zeroed workspace, no clearing launch) gives
+    the bits of musapy_cumsum_<T>_v3 on the same rows, leaves the workspace zero for the next call
+    (two calls in a row, the second smaller), and declines (-1, nothing launched) the shapes that
+    do not take the chained path."""
+    DT = {np.int64: 4, np.float32: 10, np.float64: 11}[dt]  # MUSAPY_DT_I64 / _F32 / _F64
+    ws_fn = getattr(lib(), "musapy_cumsum_ws_v1")
+    ws_fn.argtypes = [I, P, P, I, SZ, SS, I, U, U, P, U, P]
+    ws_fn.restype = ctypes.c_int
+    cs = fn(f"musapy_cumsum_{SFX[dt]}_v3", [P, P, P, I, SZ, SS, I, U, U, P])
+    WS = dev_zeros(1 << 17, np.uint64)  # 1 MiB
+    for shape in ((1030, 9000), (520, 4097)):
+        base = RNG.integers(-1000, 1001, shape, dtype=np.int64) if dt == np.int64 else RNG.random(shape).astype(dt)
+        B = ms.from_numpy(base)
+        x_ptr, sh, st = view_args(B, base, base)
+        L, total = shape[1], base.size
+        O1, O2 = dev_zeros(total, dt), dev_zeros(total, dt)
+        bpr = (L + 255) // 256
+        T = dev_zeros(shape[0] * (bpr + (bpr + 255) // 256 if bpr > 256 else bpr), dt)
+        ms.synchronize()
+        assert ws_fn(DT, x_ptr, O1.data_ptr, 2, sh, st, 1, L, total, WS.data_ptr, 1 << 20, B.stream_ptr) == 0
+        assert lib().mpy_rt_check_launch() == 0
+        cs(x_ptr, O2.data_ptr, T.data_ptr, 2, sh, st, 1, L, total, B.stream_ptr)
+        assert lib().mpy_rt_check_launch() == 0
+        ms.synchronize()
+        got = O1.numpy()[:total].reshape(shape)
+        assert_bits_equal(got, O2.numpy()[:total].reshape(shape), f"ws vs scratch entry {shape}")
+        if dt == np.int64:
+            assert_bits_equal(got, R.cumsum(base, 1), f"ws entry {shape}")
+        else:
+            want = R.cumsum(base, 1)
+            bound = TOL[dt] * np.cumsum(np.abs(base.astype(np.float64)), axis=1) + np.abs(
+                want - np.cumsum(base.astype(np.float64), axis=1))
+            assert np.all(np.abs(got.astype(np.float64) - want) <= bound), f"ws entry {shape}"
+        assert not WS.numpy().any(), "the workspace is left zero"
+    # not the chained path: few rows, a strided axis, a workspace too small
+    x = RNG.random((8, 9000)).astype(dt) if dt != np.int64 else RNG.integers(0, 9, (8, 9000))
+    X = ms.from_numpy(x)
+    x_ptr, sh, st = view_args(X, x, x)
+    O = dev_zeros(x.size, dt)
+    assert ws_fn(DT, x_ptr, O.data_ptr, 2, sh, st, 1, 9000, x.size, WS.data_ptr, 1 << 20, X.stream_ptr) == -1
+    y = RNG.random((1030, 9000)).astype(dt) if dt != np.int64 else RNG.integers(0, 9, (1030, 9000))
+    Y = ms.from_numpy(y)
+    y_ptr, sh, st = view_args(Y, y, y)
+    assert ws_fn(DT, y_ptr, O.data_ptr, 2, sh, st, 0, 1030, y.size, WS.data_ptr, 1 << 20, Y.stream_ptr) == -1
+    assert ws_fn(DT, y_ptr, O.data_ptr, 2, sh, st, 1, 9000, y.size, WS.data_ptr, 1024, Y.stream_ptr) == -1
+    assert lib().mpy_rt_check_launch() == 0
