@@ -415,9 +415,12 @@ def test_two_axis_single_launch(kind, dt):
     """max/min over (0, 1) of a C-contiguous matrix run as one launch (musapy_reduce_2d_ordered_v1)
     that must give the per-axis passes' bits: the first extreme in COLUMN-major order.  A zero of
     one sign that comes first row-major and of the other sign first column-major tells the two
-    orders apart; rows span several blocks of the persistent grid; keepdims keeps (1, 1)."""
+    orders apart; rows span several blocks of the persistent grid; keepdims keeps (1, 1).  f32 rows of
+    2048 or more elements (a multiple of 4) take the row-keyed kernel: odd row counts, rows of
+    several block rounds with a ragged end, and row 0 with and without NaN heads (the refold)."""
     sign = 1 if kind == "max" else -1
-    for shape in ((8192, 8192), (3000, 2048), (2500, 4096), (5, 8), (1, 12), (1500, 8188)):
+    for shape in ((8192, 8192), (3000, 2048), (2500, 4096), (5, 8), (1, 12), (1500, 8188), (2501, 4096),
+                  (300, 20000), (7, 2052)):
         if dt == np.int64:
             x = RNG.integers(-10**6, 10**6, shape).astype(np.int64)
         else:
