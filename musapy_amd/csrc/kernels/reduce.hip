@@ -526,38 +526,48 @@ __global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fus
 // for an f32 sum, and its 8-slot version too many registers for the two-chunk grid.  The NaN at
 // position 0 that absorbs the reduction, and the sign of a winning zero, are read back from the
 // input by the combiner.
-template <class Op, class OpF, int UNROLL, int PER>
-__global__ __launch_bounds__(kRowBS, 8) void k_reduce_all_keyed(const float* __restrict__ a, uint64_t n, uint32_t grid,
-                                                                uint64_t whole_q, uint32_t whole_r, RedOut<float> out,
-                                                                FusedArgs fa) {
-  using AF = typename OpF::A;
-  const uint32_t b = blockIdx.x;
-  if (b < grid) {
-    float first = 0.0f;
-    AF acc = all_stream<OpF, float, 4, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
-    acc = group_reduce<OpF, kRowBS>(acc, true);
-    if (threadIdx.x == 0) publish_value<2>(fa.slots + uint64_t(b) * 2, ext_key_f32<OpF>(acc));
-    return;
-  }
-  const float a0 = a[0];  // loaded while the streaming blocks run
-  // the slots in groups of at most 4 per lane (8 at once would spill): blocks are dispatched in
-  // index order, so the earlier group is published first and only the last group's wait is
-  // on the critical path
-  constexpr int kGroup = PER < 4 ? PER : 4;
-  uint64_t key = 0;
+// Keys handed over through one 64-bit word each: the word holds key + 1, so that 0 still means
+// "not published" (a key's high word never exceeds 0xff800000, so key + 1 does not wrap) and an
+// empty accumulator's key 0 travels as 1.  One word per slot instead of two tagged halves halves
+// the combiner's loads and registers: 8 slots per lane at once instead of 4.
+__device__ inline void publish_key(uint64_t* slot, uint64_t key) { st_relaxed(slot, key + 1); }
+
+// The largest of `count` published keys (lane l: slots l, l + kRowBS, ...), on thread 0, and
+// whether every slot was published within the poll budget (uniform over the block).  The slots go
+// back to zero after the block's last barrier, which would otherwise wait for those stores.
+template <int PER>
+__device__ inline bool fold_keys(uint64_t* slots, uint64_t count, uint32_t spin_limit, uint32_t* fault,
+                                 uint64_t& key) {
+  constexpr int kGroup = PER < 8 ? PER : 8;  // slots of a lane gathered at once
+  key = 0;
   bool ok = true;
 #pragma clang loop unroll(disable)
-  for (uint32_t base = 0; base < grid; base += kGroup * kRowBS) {
-    uint64_t v[kGroup][2];
-    const uint32_t cnt = grid - base < kGroup * kRowBS ? grid - base : kGroup * kRowBS;
-    ok = gather_published<2, kGroup>(fa.slots + uint64_t(base) * 2, cnt, fa.spin_limit, v) && ok;
+  for (uint64_t base = 0; base < count; base += uint64_t(kGroup) * kRowBS) {
+    uint64_t v[kGroup];
+    uint32_t pending = 0;
 #pragma unroll
     for (int j = 0; j < kGroup; ++j) {
-      const uint64_t k = (v[j][0] & 0xffffffffu) | (v[j][1] << 32);  // 0 for slots past the grid
+      v[j] = 0;
+      if (base + threadIdx.x + uint64_t(j) * kRowBS < count) pending |= 1u << j;
+    }
+    for (uint32_t spins = 0; pending != 0 && spins < spin_limit; ++spins) {
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j)
+        if (pending & (1u << j)) v[j] = ld_relaxed(slots + base + threadIdx.x + uint64_t(j) * kRowBS);
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j)
+        if (v[j] != 0) pending &= ~(1u << j);
+      if (pending) __builtin_amdgcn_s_sleep(2);
+    }
+    ok = ok && pending == 0;
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const uint64_t k = v[j] == 0 ? 0 : v[j] - 1;
       key = k > key ? k : key;
     }
   }
-  if (!combiner_gave_up(ok, fa.fault)) {  // uniform over the block
+  const bool good = !combiner_gave_up(ok, fault);
+  if (good) {
 #pragma unroll
     for (int m = kWave / 2; m >= 1; m >>= 1) {
       const uint64_t o = acc_shfl(key, m);
@@ -569,20 +579,32 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_all_keyed(const float* __r
     if (threadIdx.x == 0) {
 #pragma unroll
       for (int i = 1; i < kRowBS / kWave; ++i) key = part[i] > key ? part[i] : key;
-      AF r = ext_unkey_f32<OpF, int64_t>(key);
-      if (r.idx >= 0 && r.val == 0.0f) r.val = a[r.idx];  // the first zero's own sign
-      if (is_nan(a0)) r = AF{a0, 0};  // a NaN at position 0 absorbs the whole reduction
-      write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
     }
   }
-  // the slots go back to zero after the last barrier, which would otherwise wait for the stores
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t bb = threadIdx.x + j * kRowBS;
-    if (bb < grid) {
-      st_relaxed(fa.slots + uint64_t(bb) * 2, 0);
-      st_relaxed(fa.slots + uint64_t(bb) * 2 + 1, 0);
-    }
+  for (uint64_t bb = threadIdx.x; bb < count; bb += kRowBS) st_relaxed(slots + bb, 0);
+  return good;
+}
+
+template <class Op, class OpF, int UNROLL, int PER>
+__global__ __launch_bounds__(kRowBS, 8) void k_reduce_all_keyed(const float* __restrict__ a, uint64_t n, uint32_t grid,
+                                                                uint64_t whole_q, uint32_t whole_r, RedOut<float> out,
+                                                                FusedArgs fa) {
+  using AF = typename OpF::A;
+  const uint32_t b = blockIdx.x;
+  if (b < grid) {
+    float first = 0.0f;
+    AF acc = all_stream<OpF, float, 4, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
+    acc = group_reduce<OpF, kRowBS>(acc, true);
+    if (threadIdx.x == 0) publish_key(fa.slots + b, ext_key_f32<OpF>(acc));
+    return;
+  }
+  const float a0 = a[0];  // loaded while the streaming blocks run
+  uint64_t key;
+  if (fold_keys<PER>(fa.slots, grid, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
+    AF r = ext_unkey_f32<OpF, int64_t>(key);
+    if (r.idx >= 0 && r.val == 0.0f) r.val = a[r.idx];  // the first zero's own sign
+    if (is_nan(a0)) r = AF{a0, 0};  // a NaN at position 0 absorbs the whole reduction
+    write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
   }
 }
 
@@ -874,7 +896,7 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
   // the polls of the other blocks spread over as many memory channels
   constexpr int kFlagCopies = 64;
   uint64_t* const flag = fa.slots;
-  uint64_t* const keys = fa.slots + kFlagCopies * 32;  // one key per row (2 words)
+  uint64_t* const keys = fa.slots + kFlagCopies * 32;  // one key word per row
   if (b < R) {
     const float* row = a + b * uint64_t(C);
     __shared__ uint32_t s_nanhead;
@@ -914,51 +936,21 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
     if (threadIdx.x == 0) {
       const uint64_t key =
           acc.idx < 0 ? 0 : ext_key_f32<OpF>(AF{acc.val, int64_t(acc.idx) * int64_t(R) + int64_t(b)});
-      publish_value<2>(keys + b * 2, key);
+      publish_key(keys + b, key);
     }
     return;
   }
-  // combiner: the R keys, in groups of at most 4 per lane (see k_reduce_all_keyed)
+  // combiner: the R row keys
   const float a0 = a[0];
-  constexpr int kGroup = PER < 4 ? PER : 4;
-  uint64_t key = 0;
-  bool ok = true;
-#pragma clang loop unroll(disable)
-  for (uint64_t base = 0; base < R; base += kGroup * kRowBS) {
-    uint64_t v[kGroup][2];
-    const uint32_t cnt = uint32_t(R - base < kGroup * kRowBS ? R - base : kGroup * kRowBS);
-    ok = gather_published<2, kGroup>(keys + base * 2, cnt, fa.spin_limit, v) && ok;
-#pragma unroll
-    for (int j = 0; j < kGroup; ++j) {
-      const uint64_t kk = (v[j][0] & 0xffffffffu) | (v[j][1] << 32);
-      key = kk > key ? kk : key;
+  uint64_t key;
+  if (fold_keys<PER>(keys, R, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
+    AF r = ext_unkey_f32<OpF, int64_t>(key);
+    if (r.idx >= 0 && r.val == 0.0f) {  // the first zero's own sign
+      const uint64_t col = uint64_t(r.idx) / R, rw = uint64_t(r.idx) % R;
+      r.val = a[rw * uint64_t(C) + col];
     }
-  }
-  if (!combiner_gave_up(ok, fa.fault)) {  // uniform over the block
-#pragma unroll
-    for (int m = kWave / 2; m >= 1; m >>= 1) {
-      const uint64_t o = acc_shfl(key, m);
-      key = o > key ? o : key;
-    }
-    __shared__ uint64_t part[kRowBS / kWave];
-    if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = key;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-#pragma unroll
-      for (int i = 1; i < kRowBS / kWave; ++i) key = part[i] > key ? part[i] : key;
-      AF r = ext_unkey_f32<OpF, int64_t>(key);
-      if (r.idx >= 0 && r.val == 0.0f) {  // the first zero's own sign
-        const uint64_t col = uint64_t(r.idx) / R, rw = uint64_t(r.idx) % R;
-        r.val = a[rw * uint64_t(C) + col];
-      }
-      if (is_nan(a0)) r = AF{a0, 0};  // column 0 is NaN: it absorbs the second pass
-      write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
-    }
-  }
-  // the slots go back to zero after the last barrier
-  for (uint64_t bb = threadIdx.x; bb < R; bb += kRowBS) {
-    st_relaxed(keys + bb * 2, 0);
-    st_relaxed(keys + bb * 2 + 1, 0);
+    if (is_nan(a0)) r = AF{a0, 0};  // column 0 is NaN: it absorbs the second pass
+    write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
   }
   if (threadIdx.x < kFlagCopies) st_relaxed(flag + threadIdx.x * 32, 0);
 }
@@ -1265,7 +1257,7 @@ int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, siz
     if (n < 0xffffffffull) {  // one key per block, the grid of one-word accumulators
       uint64_t kg = ceil_div(nchunks, uint64_t(2));
       if (kg > kAllMaxBlocks) kg = kAllMaxBlocks;
-      if (kg >= 2 && kg * 2 * 8 <= ws_bytes) {
+      if (kg >= 2 && kg * 8 <= ws_bytes) {
         const uint32_t g = uint32_t(kg);
         const uint64_t q = (n / kChunk) / kg;
         const uint32_t r = uint32_t((n / kChunk) % kg);
@@ -1316,7 +1308,7 @@ int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, 
   if constexpr (std::is_same_v<T, float>) {
     // rows of at least one block round: the row-keyed kernel
     if (C >= 2048 && C % 4 == 0 && C < (uint64_t(1) << 31) && R * C < 0xffffffffull && al16(a) &&
-        (64 * 32 + R * 2) * 8 <= ws_bytes) {
+        (64 * 32 + R) * 8 <= ws_bytes) {
       FusedArgs fk{};
       fk.slots = static_cast<uint64_t*>(ws);
       fk.fault = device_fault_word(st);
@@ -1329,8 +1321,10 @@ int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, 
         k_reduce_rows2d_keyed<OpR, OpF, 4, 1><<<g, kRowBS, 0, st>>>(a, R, uint32_t(C), out, fk);
       else if (per == 2)
         k_reduce_rows2d_keyed<OpR, OpF, 4, 2><<<g, kRowBS, 0, st>>>(a, R, uint32_t(C), out, fk);
-      else
+      else if (per <= 4)
         k_reduce_rows2d_keyed<OpR, OpF, 4, 4><<<g, kRowBS, 0, st>>>(a, R, uint32_t(C), out, fk);
+      else
+        k_reduce_rows2d_keyed<OpR, OpF, 4, 8><<<g, kRowBS, 0, st>>>(a, R, uint32_t(C), out, fk);
       return kFusedLaunched;
     }
   }
