@@ -343,9 +343,11 @@ int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_
  * and signed-zero outcomes included: the first extreme element in column-major order, among the
  * non-NaN elements of the columns whose row-0 element is not NaN, or a[0][0] when that is NaN.
  * `op` is MUSAPY_RED_MAX or MUSAPY_RED_MIN; `workspace` follows musapy_reduce_fused_v1's rules
- * (zero before the first call, left zero; 1024 slots of 4 words at most).  Returns 0 when
- * launched, -1 when not covered (more than 1024 groups of 64 16-byte column vectors, or rows >=
- * 2^31): then reduce per axis. */
+ * (zero before the first call, left zero).  f32 arrays with cols >= 2048 (a multiple of 4, 16-byte
+ * aligned, rows * cols < 2^32 - 1) run as keyed rows and use (2048 + rows) 64-bit words; other
+ * shapes use the column tiling and at most 1024 slots of 4 words.  Returns 0 when launched, -1
+ * when not covered (more than 1024 groups of 64 16-byte column vectors, or rows >= 2^31): then
+ * reduce per axis. */
 int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_t rows, size_t cols, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- single-launch reduction that allocates nothing (new; no counterpart in kernels.rs) ----

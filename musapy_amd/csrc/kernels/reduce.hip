@@ -843,10 +843,10 @@ __global__ __launch_bounds__(BS) void k_reduce_col2d(const T* __restrict__ a, Co
 // among those columns' non-NaN elements, and a row's extreme at its first column, keyed
 // (value, column * R + row) (ext_key_f32), is the candidate of that row in column-major order.  Each
 // block publishes its key; the last block folds the R keys with unsigned maxima and reads the
-// winning zero's sign, and x[0][0] when it is NaN, back from the input.  (8192, 8192) event-timed:
-// 47.0 us against 54.2 us for the column-strip kernel (k_reduce_col2d, still used for f64, i64 and
-// short rows); a timing copy that skipped the NaN-head columns altogether took 46.2-46.7 us.  Two
-// rows per block measured slower (52 us: the two rows' registers spill at 8 waves per SIMD).
+// winning zero's sign, and x[0][0] when it is NaN, back from the input.  (8192, 8192): kernel
+// 43.9 us, 44.5 us event-timed, against 54.2 us for the column-strip kernel (k_reduce_col2d, still
+// used for f64, i64 and short rows).  Two rows per block measured slower (52 us: the two rows'
+// registers spill at 8 waves per SIMD).
 // One lane's extreme over row `row` of C f32 elements (C a multiple of 4), in the row kernel's
 // access pattern; with `masked`, elements of columns whose row-0 element (in `a`) is NaN are
 // skipped like NaNs.
@@ -1296,8 +1296,9 @@ int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, siz
 }
 
 
-// max / min over both axes of a C-contiguous (R, C) array in one launch (k_reduce_col2d), with
-// the column kernel's tiling (about 256 blocks); kFusedNotCovered when the shape does not fit it
+// max / min over both axes of a C-contiguous (R, C) array in one launch: f32 rows of at least
+// 2048 elements as keyed rows (k_reduce_rows2d_keyed, R + 1 blocks), the rest with the column
+// kernel's tiling (k_reduce_col2d, about 256 blocks); kFusedNotCovered when the shape fits neither
 template <class Op, class OpF, class T>
 int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, void* ws, size_t ws_bytes,
                              hipStream_t st) {
