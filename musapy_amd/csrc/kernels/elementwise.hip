@@ -22,6 +22,12 @@
 namespace mpy {
 
 constexpr int kBlock = 256;
+// Lanes per block of the flat kernels (unit-stride operands, one vector per lane).  Measured on
+// MI355X with streaming stores: binary ops run faster in 128-lane blocks (64M f32 add 124.2 ->
+// 119.4 us, c128 mul 124.4 -> 119.7, the i64 + f64 add 62.5 -> 60.1, 16M f32 add 33.4 -> 32.9),
+// unary ops and casts slower (clamp of 16M f64 43.3 -> 44.1, f64 -> f32 34.1 -> 34.6).
+constexpr int kFlatBlockUnary = 256;
+constexpr int kFlatBlockBinary = 128;
 
 // ---------------------------------------------------------------------------------------------
 // operand access modes
@@ -38,9 +44,9 @@ struct In {
 // ---------------------------------------------------------------------------------------------
 // flat: 1-D, every input contiguous (mode 1) or scalar (mode 0).  Full tiles use VEC-wide
 // vector accesses; the final partial tile falls back to one element per lane.
-template <int VEC, int UNROLL, class F, class TO, class TA>
-__global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict__ c, uint64_t n, bool nts, F f) {
-  constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
+template <int VEC, int UNROLL, bool NTS, class F, class TO, class TA>
+__global__ __launch_bounds__(kFlatBlockUnary) void k_unary_flat(In<TA> a, TO* __restrict__ c, uint64_t n, F f) {
+  constexpr uint64_t kTile = uint64_t(kFlatBlockUnary) * VEC * UNROLL;
   const uint64_t base = uint64_t(blockIdx.x) * kTile;
   const int t = threadIdx.x;
   if (base + kTile <= n) {
@@ -52,26 +58,25 @@ __global__ __launch_bounds__(kBlock) void k_unary_flat(In<TA> a, TO* __restrict_
 #pragma unroll
         for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
     } else {
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) va[u] = vload_pol<TA, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC, a.nt);
+      static_for<UNROLL>(
+          [&](auto u) { va[u] = vload_pol<TA, VEC>(a.p + base + uint64_t(u * kFlatBlockUnary + t) * VEC, a.nt); });
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
+    static_for<UNROLL>([&](auto u) {
       Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k]);
-      vstore_pol<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc, nts);
-    }
+      vstore_as<NTS, TO, VEC>(c + base + uint64_t(u * kFlatBlockUnary + t) * VEC, vc);
+    });
   } else {
-    for (uint64_t i = base + t; i < n; i += kBlock) c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i]);
+    for (uint64_t i = base + t; i < n; i += kFlatBlockUnary) c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i]);
   }
 }
 
 // TO: the output element type (T for arithmetic, uint8_t for comparisons)
-template <int VEC, int UNROLL, class F, class T, class TO = T>
-__global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __restrict__ c, uint64_t n, bool nts,
-                                                        F f) {
-  constexpr uint64_t kTile = uint64_t(kBlock) * VEC * UNROLL;
+template <int VEC, int UNROLL, bool NTS, class F, class T, class TO = T>
+__global__ __launch_bounds__(kFlatBlockBinary) void k_binary_flat(In<T> a, In<T> b, TO* __restrict__ c, uint64_t n,
+                                                                  F f) {
+  constexpr uint64_t kTile = uint64_t(kFlatBlockBinary) * VEC * UNROLL;
   const uint64_t base = uint64_t(blockIdx.x) * kTile;
   const int t = threadIdx.x;
   if (base + kTile <= n) {
@@ -83,8 +88,8 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __
 #pragma unroll
         for (int k = 0; k < VEC; ++k) va[u].v[k] = s;
     } else {
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) va[u] = vload_pol<T, VEC>(a.p + base + uint64_t(u * kBlock + t) * VEC, a.nt);
+      static_for<UNROLL>(
+          [&](auto u) { va[u] = vload_pol<T, VEC>(a.p + base + uint64_t(u * kFlatBlockBinary + t) * VEC, a.nt); });
     }
     if (b.mode == kModeScalar) {
       const T s = b.p[0];
@@ -93,18 +98,17 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(In<T> a, In<T> b, TO* __
 #pragma unroll
         for (int k = 0; k < VEC; ++k) vb[u].v[k] = s;
     } else {
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) vb[u] = vload_pol<T, VEC>(b.p + base + uint64_t(u * kBlock + t) * VEC, b.nt);
+      static_for<UNROLL>(
+          [&](auto u) { vb[u] = vload_pol<T, VEC>(b.p + base + uint64_t(u * kFlatBlockBinary + t) * VEC, b.nt); });
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
+    static_for<UNROLL>([&](auto u) {
       Vec<TO, VEC> vc;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) vc.v[k] = f(va[u].v[k], vb[u].v[k]);
-      vstore_pol<TO, VEC>(c + base + uint64_t(u * kBlock + t) * VEC, vc, nts);
-    }
+      vstore_as<NTS, TO, VEC>(c + base + uint64_t(u * kFlatBlockBinary + t) * VEC, vc);
+    });
   } else {
-    for (uint64_t i = base + t; i < n; i += kBlock)
+    for (uint64_t i = base + t; i < n; i += kFlatBlockBinary)
       c[i] = f(a.mode == kModeScalar ? a.p[0] : a.p[i], b.mode == kModeScalar ? b.p[0] : b.p[i]);
   }
 }
@@ -137,10 +141,9 @@ __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t co
   }
 }
 
-template <int VEC, int UNROLL, class F, class TO, class TA>
+template <int VEC, int UNROLL, bool NTS, class F, class TO, class TA>
 __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO* __restrict__ c, RowIndexer<2> ix,
-                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, bool nts,
-                                                       F f) {
+                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, F f) {
   const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k]);
-      vstore_pol<TO, VEC>(cp, v, nts);
+      vstore_as<NTS, TO, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -167,10 +170,10 @@ __global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO*
   }
 }
 
-template <int VEC, int UNROLL, class F, class T, class TO = T>
+template <int VEC, int UNROLL, bool NTS, class F, class T, class TO = T>
 __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<T> b, int64_t sb, TO* __restrict__ c,
                                                         RowIndexer<3> ix, FastDiv gpr, uint32_t L, uint32_t items,
-                                                        bool aligned, bool nts, F f) {
+                                                        bool aligned, F f) {
   const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(x[k], y[k]);
-      vstore_pol<TO, VEC>(cp, v, nts);
+      vstore_as<NTS, TO, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -201,10 +204,11 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
 // ---------------------------------------------------------------------------------------------
 // mixed dtypes: c = f(TC(a), TC(b)) with the cast functors of the cast kernels, i.e. exactly the
 // reference's cast-then-compute (op_builder.rs:410-417) without materialising the cast.
-template <int VEC, class F, class TC, class TA, class TB>
-__global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restrict__ a, const TB* __restrict__ b,
-                                                              TC* __restrict__ c, uint64_t n, bool nt, bool nts, F f) {
-  const uint64_t i0 = (uint64_t(blockIdx.x) * kBlock + threadIdx.x) * VEC;
+template <int VEC, bool NTS, class F, class TC, class TA, class TB>
+__global__ __launch_bounds__(kFlatBlockBinary) void k_binary_flat_mixed(const TA* __restrict__ a,
+                                                                        const TB* __restrict__ b,
+                                                              TC* __restrict__ c, uint64_t n, bool nt, F f) {
+  const uint64_t i0 = (uint64_t(blockIdx.x) * kFlatBlockBinary + threadIdx.x) * VEC;
   const CastF<TA, TC> ca{};
   const CastF<TB, TC> cb{};
   if (i0 + VEC <= n) {
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat_mixed(const TA* __restri
     Vec<TC, VEC> z;
 #pragma unroll
     for (int k = 0; k < VEC; ++k) z.v[k] = f(ca(x.v[k]), cb(y.v[k]));
-    vstore_pol<TC, VEC>(c + i0, z, nts);
+    vstore_as<NTS, TC, VEC>(c + i0, z);
   } else {
     for (uint64_t i = i0; i < n; ++i) c[i] = f(ca(a[i]), cb(b[i]));
   }
@@ -232,10 +236,9 @@ struct RowPieceArgs {
   uint32_t L;         // row length (innermost output dim)
   FastDiv groups;     // blocks per row
   bool aligned;       // every item full and 16-byte aligned (host-checked)
-  bool nts;           // streaming stores
 };
 
-template <int VEC, int U, class F, class T, class TO = T>
+template <int VEC, int U, bool NTS, class F, class T, class TO = T>
 __global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa, In<T> b, int64_t sb,
                                                              TO* __restrict__ c, RowPieceArgs ra, F f) {
   const uint32_t row = fd_div(ra.groups, blockIdx.x);
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa
       Vec<TO, VEC> v;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) v.v[k] = f(xa[u][k], xb[u][k]);
-      vstore_pol<TO, VEC>(cp, v, ra.nts);
+      vstore_as<NTS, TO, VEC>(cp, v);
     } else {
 #pragma unroll
       for (int k = 0; k < VEC; ++k)
@@ -280,7 +283,6 @@ struct TransposeArgs {
   RowIndexer<2> batch;     // batch dims: [0] output strides, [1] input strides
   bool vec_in, vec_out;    // 16-byte aligned vector access possible on each side
   bool nt;                 // streaming loads
-  bool nts;                // streaming stores
 };
 
 // Tile geometry: PL lanes x VI elements along P (input-contiguous) by TL along L
@@ -290,7 +292,7 @@ struct TransposeArgs {
 template <class T> constexpr int tr_vec() { return sizeof(T) >= 16 ? 1 : (sizeof(T) == 1 ? 8 : int(16 / sizeof(T))); }
 template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
 
-template <class F, class TO, class TI, int PL, int TL>
+template <class F, class TO, class TI, int PL, int TL, bool NTS>
 __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
                                                             TransposeArgs ta, F f) {
   constexpr int VI = tr_vec<TI>(), VO = tr_vec<TO>();
@@ -357,7 +359,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
         Vec<TO, VO> v;
 #pragma unroll
         for (int q = 0; q < VO; ++q) v.v[q] = tile[ll + q][pp];
-        vstore_pol<TO, VO>(dst, v, ta.nts);
+        vstore_as<NTS, TO, VO>(dst, v);
       } else {
 #pragma unroll
         for (int q = 0; q < VO; ++q)
@@ -370,24 +372,26 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
 // Launches the tiled transpose with tile (PL lanes along P) x TL; the tile is narrowed along P
 // (and lengthened along L, same LDS bytes) when P is small, so that no tile is mostly empty.
 template <class F, class TO, class TI, int PL, int TL>
-bool launch_transpose_tiles(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, hipStream_t st, F f) {
+bool launch_transpose_tiles(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, bool nts, hipStream_t st, F f) {
   constexpr uint64_t TP = tr_tp<TI, PL>();
   const uint64_t tL = (ta.L + TL - 1) / TL, tP = (ta.P + TP - 1) / TP;
   if (tL * tP * nb >= (uint64_t(1) << 31)) return false;
   ta.tilesL = make_fastdiv(uint32_t(tL));
   ta.tilesP = make_fastdiv(uint32_t(tP));
-  k_unary_transpose<F, TO, TI, PL, TL><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
+  with_store_policy(nts, [&](auto NT) {
+    k_unary_transpose<F, TO, TI, PL, TL, NT.value><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
+  });
   return true;
 }
 
 template <class F, class TO, class TI>
-bool launch_transpose(const TI* a, TO* c, const TransposeArgs& ta, uint64_t nb, hipStream_t st, F f) {
+bool launch_transpose(const TI* a, TO* c, const TransposeArgs& ta, uint64_t nb, bool nts, hipStream_t st, F f) {
   // LDS per tile: TL x (PL*VI + 1) elements of TO; 32 lanes x 64 rows is 33 KB for f32
   if (ta.P * 4 <= uint64_t(tr_tp<TI, 32>()))
-    return launch_transpose_tiles<F, TO, TI, 8, 256>(a, c, ta, nb, st, f);
+    return launch_transpose_tiles<F, TO, TI, 8, 256>(a, c, ta, nb, nts, st, f);
   if (ta.P * 2 <= uint64_t(tr_tp<TI, 32>()))
-    return launch_transpose_tiles<F, TO, TI, 16, 128>(a, c, ta, nb, st, f);
-  return launch_transpose_tiles<F, TO, TI, 32, 64>(a, c, ta, nb, st, f);
+    return launch_transpose_tiles<F, TO, TI, 16, 128>(a, c, ta, nb, nts, st, f);
+  return launch_transpose_tiles<F, TO, TI, 32, 64>(a, c, ta, nb, nts, st, f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -533,16 +537,20 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
   // the narrower type moves 16 bytes per item, the wider one 16-32 (e.g. f64->f32: 4 elements)
   constexpr int V = ew_vec<TA, TO>();
   const bool nt = operand_elems(p, 1) * sizeof(TA) >= kStreamLoadBytes;
-  const bool nts = p.numel * sizeof(TO) >= kStreamStoreBytes;
+  const bool nts = p.numel * sizeof(TO) >= kStreamStoreBytesUnary;
   if (p.ndim == 1 && p.stride[0][0] == 1 && (p.stride[1][0] == 0 || p.stride[1][0] == 1)) {
     In<TA> ia{a, mode_of(p.stride[1][0]), nt};
     bool vec_ok = aligned16(c) && (ia.mode == kModeScalar || aligned16(a));
     if (vec_ok) {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
-      k_unary_flat<V, kFlatUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, nts, f);
+      constexpr uint64_t kTile = uint64_t(kFlatBlockUnary) * V * kFlatUnroll;
+      const uint64_t tiles = (p.numel + kTile - 1) / kTile;
+      with_store_policy(nts, [&](auto NT) {
+        k_unary_flat<V, kFlatUnroll, NT.value, F, TO, TA><<<dim3(unsigned(tiles)), kFlatBlockUnary, 0, st>>>(
+            ia, c, p.numel, f);
+      });
     } else {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
-      k_unary_flat<1, kUnroll, F, TO, TA><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, c, p.numel, nts, f);
+      uint64_t tiles = (p.numel + uint64_t(kFlatBlockUnary) * kUnroll - 1) / (uint64_t(kFlatBlockUnary) * kUnroll);
+      k_unary_flat<1, kUnroll, false, F, TO, TA><<<dim3(unsigned(tiles)), kFlatBlockUnary, 0, st>>>(ia, c, p.numel, f);
     }
     return;
   }
@@ -566,7 +574,6 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
         ta.vec_in = aligned16(a) && (uint64_t(sL < 0 ? -sL : sL) * sizeof(TA)) % 16 == 0;
         ta.vec_out = aligned16(c) && (uint64_t(ta.out_sP) * sizeof(TO)) % 16 == 0;
         ta.nt = true;  // tiles read across many rows at once: streaming won at 128 MB too (5.1 vs 4.9 TB/s)
-        ta.nts = nts;
         for (int d = nd - 2; d >= 0; --d) {
           if (d == P) continue;
           int k = ta.batch.nd++;
@@ -576,7 +583,7 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
           if ((uint64_t(p.stride[1][d] < 0 ? -p.stride[1][d] : p.stride[1][d]) * sizeof(TA)) % 16) ta.vec_in = false;
           if ((uint64_t(p.stride[0][d]) * sizeof(TO)) % 16) ta.vec_out = false;
         }
-        if (launch_transpose<F, TO, TA>(a, c, ta, nb, st, f)) return;
+        if (launch_transpose<F, TO, TA>(a, c, ta, nb, nts, st, f)) return;
       }
     }
   }
@@ -588,8 +595,10 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<2> ix = make_row_indexer<2>(p);
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-    k_unary_rows<V, kUnroll, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items, al, nts,
-                                                                 f);
+    with_store_policy(nts, [&](auto NT) {
+      k_unary_rows<V, kUnroll, NT.value, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items,
+                                                                           al, f);
+    });
     return;
   }
   k_unary_generic<F, TO, TA><<<grid_generic(p.numel), kBlock, 0, st>>>(a, c, make_meta64(p), p.numel, f);
@@ -611,11 +620,16 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
     bool vec_ok = (reinterpret_cast<uintptr_t>(c) % kOutAlign) == 0 && (ia.mode == kModeScalar || aligned16(a)) &&
                   (ib.mode == kModeScalar || aligned16(b));
     if (vec_ok) {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * V * kFlatUnroll - 1) / (uint64_t(kBlock) * V * kFlatUnroll);
-      k_binary_flat<V, kFlatUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, nts, f);
+      constexpr uint64_t kTile = uint64_t(kFlatBlockBinary) * V * kFlatUnroll;
+      const uint64_t tiles = (p.numel + kTile - 1) / kTile;
+      with_store_policy(nts, [&](auto NT) {
+        k_binary_flat<V, kFlatUnroll, NT.value, F, T, TO><<<dim3(unsigned(tiles)), kFlatBlockBinary, 0, st>>>(
+            ia, ib, c, p.numel, f);
+      });
     } else {
-      uint64_t tiles = (p.numel + uint64_t(kBlock) * kUnroll - 1) / (uint64_t(kBlock) * kUnroll);
-      k_binary_flat<1, kUnroll, F, T, TO><<<dim3(unsigned(tiles)), kBlock, 0, st>>>(ia, ib, c, p.numel, nts, f);
+      uint64_t tiles = (p.numel + uint64_t(kFlatBlockBinary) * kUnroll - 1) / (uint64_t(kFlatBlockBinary) * kUnroll);
+      k_binary_flat<1, kUnroll, false, F, T, TO><<<dim3(unsigned(tiles)), kFlatBlockBinary, 0, st>>>(ia, ib, c,
+                                                                                                     p.numel, f);
     }
     return;
   }
@@ -634,18 +648,22 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
       ra.ix = ix;
       ra.L = L;
       ra.aligned = al;
-      ra.nts = nts;
       const uint32_t groups = (L + uint32_t(kBlock) * V * U - 1) / (uint32_t(kBlock) * V * U);
       ra.groups = make_fastdiv(groups);
       const uint64_t blocks = uint64_t(p.numel / L) * groups;
       if (blocks < (uint64_t(1) << 31)) {
-        k_binary_rowpieces<V, U, F, T, TO><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(ia, sa, ib, sb, c, ra, f);
+        with_store_policy(nts, [&](auto NT) {
+          k_binary_rowpieces<V, U, NT.value, F, T, TO><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(ia, sa, ib, sb, c,
+                                                                                                  ra, f);
+        });
         return;
       }
     }
     unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-    k_binary_rows<V, kUnroll, F, T, TO><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr), L, items, al,
-                                                                 nts, f);
+    with_store_policy(nts, [&](auto NT) {
+      k_binary_rows<V, kUnroll, NT.value, F, T, TO><<<grid, kBlock, 0, st>>>(ia, sa, ib, sb, c, ix, make_fastdiv(gpr),
+                                                                           L, items, al, f);
+    });
     return;
   }
   k_binary_generic<F, T, TO><<<grid_generic(p.numel), kBlock, 0, st>>>(a, b, c, make_meta64(p), p.numel, f);
@@ -663,10 +681,13 @@ void launch_binary_mixed(const void* a, const void* b, void* c, int ndim, const 
   constexpr int V = 16 / (sizeof(TA) > sizeof(TB) ? (sizeof(TA) > sizeof(TC) ? sizeof(TA) : sizeof(TC))
                                                   : (sizeof(TB) > sizeof(TC) ? sizeof(TB) : sizeof(TC)));
   if (p.ndim == 1 && p.stride[1][0] == 1 && p.stride[2][0] == 1 && aligned16(a) && aligned16(b) && aligned16(c)) {
-    const uint64_t blocks = (p.numel + uint64_t(kBlock) * V - 1) / (uint64_t(kBlock) * V);
+    const uint64_t blocks = (p.numel + uint64_t(kFlatBlockBinary) * V - 1) / (uint64_t(kFlatBlockBinary) * V);
     const bool nt = p.numel * (sizeof(TA) + sizeof(TB)) >= kStreamLoadBytes;
     const bool nts = p.numel * sizeof(TC) >= kStreamStoreBytes;
-    k_binary_flat_mixed<V, F, TC, TA, TB><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(pa, pb, pc, p.numel, nt, nts, f);
+    with_store_policy(nts, [&](auto NT) {
+      k_binary_flat_mixed<V, NT.value, F, TC, TA, TB><<<dim3(unsigned(blocks)), kFlatBlockBinary, 0, st>>>(
+          pa, pb, pc, p.numel, nt, f);
+    });
     return;
   }
   k_binary_generic_mixed<F, TC, TA, TB><<<grid_generic(p.numel), kBlock, 0, st>>>(pa, pb, pc, make_meta64(p),

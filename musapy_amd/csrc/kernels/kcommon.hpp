@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 #include <stddef.h>
 #include <sys/types.h>
 
@@ -129,15 +130,42 @@ __device__ inline Vec<T, N> vload_pol(const T* p, bool nt) {
   return nt ? vload_nt<T, N>(p) : vload<T, N>(p);
 }
 
-// Store policy of the elementwise kernels by volume: an output of at least this many bytes is
-// written with streaming stores.  Such an output does not stay in the 256 MB Infinity Cache for
-// its consumer anyway; measured on MI355X with outputs rotated over 4 buffers, streaming stores
-// moved the (8192, 8192) f32 transpose 112.5 -> 107 us, a flip 98 -> 91 us, the c128 transpose
-// 111 -> 102 us and c128 mul/div 130 -> 124 us, and left the other configs unchanged.
+// Store policy by volume: an output of at least this many bytes is written with streaming
+// stores (binary ops and scans; unary ops and casts from kStreamStoreBytesUnary).  Such an output
+// does not stay in the 256 MB Infinity Cache for its consumer anyway.  Measured on MI355X with
+// inputs and outputs rotated over 4 buffers, against default stores: 64M f32 add 130 -> 120 us,
+// the i64 + f64 add of 16M 66.5 -> 61.5, c128 mul 129 -> 121, the (8192, 8192) f32 transpose
+// 113 -> 107, a flip 97.5 -> 91.5, the c128 transpose 110.5 -> 102.5, C5's cumsum 195 -> 188,
+// C2's broadcast add 24.7 -> 23.1, 16M f32 add 33.6 -> 32.3 us (with 128-lane blocks).  Unary
+// ops with a 64 MB output measured slower streamed (f64 -> f32 of 16M 34.2 against 33.3 us, c64
+// abs 34.0 against 33.2), so they stream from 128 MB (clamp of 16M f64: 44.7 -> 42.7 us).
 constexpr uint64_t kStreamStoreBytes = uint64_t(64) << 20;
-template <typename T, int N>
-__device__ inline void vstore_pol(T* p, const Vec<T, N>& v, bool nt) {
-  if (nt) vstore_nt<T, N>(p, v); else vstore<T, N>(p, v);
+constexpr uint64_t kStreamStoreBytesUnary = uint64_t(128) << 20;
+// The store policy is a template parameter, not a runtime flag: the compiler merges a runtime
+// choice between a streaming and a default store of the same value to the same address into one
+// default store (the two branches are combined and the nontemporal hint is dropped), which left
+// every kernel of this library without streaming stores until the policy was made static.
+template <bool NT, typename T, int N>
+__device__ inline void vstore_as(T* p, const Vec<T, N>& v) {
+  if constexpr (NT) vstore_nt<T, N>(p, v); else vstore<T, N>(p, v);
+}
+
+// Calls fn(std::integral_constant<int, 0>{}) .. fn(std::integral_constant<int, N - 1>{}) as
+// straight-line code.  For loops around streaming stores: the compiler promotes a store out of a
+// one-trip loop (N = 1) and drops its nontemporal hint on the way.
+template <int N, int I = 0, class Fn>
+__device__ inline void static_for(Fn&& fn) {
+  if constexpr (I < N) {
+    fn(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(fn);
+  }
+}
+
+// Calls `launch` with std::true_type or std::false_type: a kernel template's store policy from
+// the launcher's runtime decision.
+template <class L>
+inline void with_store_policy(bool nt, L&& launch) {
+  if (nt) launch(std::true_type{}); else launch(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -298,10 +298,10 @@ struct ChainArgs {
   uint32_t* fault;      // the device's fault word (kcommon.hpp)
   uint32_t spin_limit;  // polls a wait may make
   bool vec;             // 16-byte aligned rows
-  bool nt_load, nt_store;
+  bool nt_load;
 };
 
-template <class T, int BS, int VPT>
+template <class T, int BS, int VPT, bool NTS>
 __global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* __restrict__ c, ChainArgs sa) {
   using A = typename ScanAcc<T>::A;
   constexpr int VE = int(16 / sizeof(T));
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* _
       Vec<T, VE> v;
 #pragma unroll
       for (int e = 0; e < VE; ++e) v.v[e] = T(P + (lane_off[u] + x[u][e]));
-      vstore_pol<T, VE>(cout + t0 + (uint64_t(u) * BS + tid) * VE, v, sa.nt_store);
+      vstore_as<NTS, T, VE>(cout + t0 + (uint64_t(u) * BS + tid) * VE, v);
     }
   } else {
 #pragma unroll
@@ -536,7 +536,6 @@ void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_
   ca.vec = sh.vec;
   const uint64_t bytes = uint64_t(p.rows) * p.L * sizeof(T);
   ca.nt_load = bytes >= kStreamLoadBytes;
-  ca.nt_store = bytes >= kStreamStoreBytes;
   if (ca.fault == nullptr) {  // a wait that ran out could not be reported: take no waits
     g_wrapper_error = 1;
     return;
@@ -545,7 +544,9 @@ void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_
     unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
     k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
   }
-  k_scan_chain<T, kChainBlock, kChainVpt><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
+  with_store_policy(bytes >= kStreamStoreBytes, [&](auto NT) {
+    k_scan_chain<T, kChainBlock, kChainVpt, NT.value><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
+  });
 }
 
 template <class T>
