@@ -1,5 +1,6 @@
-"""The built kernels really issue streaming stores, on CPU: the gfx950 code objects of the build
-are disassembled and the kernel instantiations that a launcher selects for large outputs must hold
+"""The built kernels really issue streaming stores, on CPU: the gfx950 code objects that
+`__graft_entry__.build()` compiled in this tree from its own sources (musapy_amd/_build) are
+disassembled, and the kernel instantiations that a launcher selects for large outputs must hold
 `global_store_... nt` instructions.  A runtime choice between a streaming and a default store was
 once merged by the compiler into a default store in every kernel, silently (results are the same,
 only the HBM rate drops), and a one-trip loop around the store loses the hint the same way."""
