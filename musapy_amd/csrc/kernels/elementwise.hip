@@ -287,21 +287,43 @@ struct TransposeArgs {
 
 // Tile geometry: PL lanes x VI elements along P (input-contiguous) by TL along L
 // (output-contiguous); VI / VO = elements per vector: 16 bytes, 8 for 1-byte types (which keeps
-// a u8 -> f64 tile inside LDS).  A pass of the read phase covers kBlock / PL rows of L, a pass
-// of the write phase kBlock / (TL / VO) rows of P.
+// a u8 -> f64 tile inside LDS).  A pass of the read phase covers kTrBlock / PL rows of L, a pass
+// of the write phase kTrBlock / (TL / VO) rows of P.
 template <class T> constexpr int tr_vec() { return sizeof(T) >= 16 ? 1 : (sizeof(T) == 1 ? 8 : int(16 / sizeof(T))); }
 template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
+// Block shapes, measured on MI355X with streaming loads and stores and rotated outputs:
+//  * copies and casts, 32 lanes along P: 1024-lane blocks over 128-row tiles (512-byte runs on
+//    both sides for 4-byte types; about 66 KB of LDS, two blocks per CU).  (8192, 8192) f32
+//    transposed: 91.5 us, against 106.6-107.5 us for the previous 64-row tiles in 256 lanes and
+//    97.4-97.9 us in 512 lanes; the c128 transpose 94.8 against 102.5 us;
+//  * other functors (exp of a transposed view): 512 lanes over 64-row tiles, 50.0-50.3 us for
+//    C2's exp against 52.9 us with the copy shape (the functor's work favours more, smaller tiles);
+//  * 16 or 8 lanes along P (small P): 1024 lanes over 128- or 256-row tiles (the (8192, 128, 64)
+//    permute: 91.0-92.1 us, against 95.1 us over 256 rows).
+// The rows are halved until the tile's LDS fits in 68 KB (wide outputs of narrow inputs).
+template <class F> struct tr_moves_only : std::false_type {};  // copies and casts
+template <> struct tr_moves_only<IdentityF> : std::true_type {};
+template <class S, class D> struct tr_moves_only<CastF<S, D>> : std::true_type {};
+template <> struct tr_moves_only<ToBf16F> : std::true_type {};
+template <> struct tr_moves_only<ToF16F> : std::true_type {};
+template <class TO, class TI, int PL, int BS, int ROWS>
+constexpr int tr_tl() {
+  constexpr uint64_t TP = tr_tp<TI, PL>();
+  int tl = ROWS;
+  while (tl > BS / PL && uint64_t(tl) * (TP + 1) * sizeof(TO) > 68 * 1024) tl /= 2;
+  return tl;
+}
 
-template <class F, class TO, class TI, int PL, int TL, bool NTS>
-__global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
+template <class F, class TO, class TI, int PL, int TL, int BS, bool NTS>
+__global__ __launch_bounds__(BS) void k_unary_transpose(const TI* __restrict__ a, TO* __restrict__ c,
                                                             TransposeArgs ta, F f) {
   constexpr int VI = tr_vec<TI>(), VO = tr_vec<TO>();
   constexpr int TP = tr_tp<TI, PL>();
-  constexpr int RP = kBlock / PL;  // L rows per read pass
-  static_assert(kBlock % PL == 0 && TL % RP == 0, "read passes must tile TL");
+  constexpr int RP = BS / PL;  // L rows per read pass
+  static_assert(BS % PL == 0 && TL % RP == 0, "read passes must tile TL");
   constexpr int NRP = TL / RP;
   constexpr int LPW = TL / VO;     // lanes along one output row
-  static_assert(kBlock % LPW == 0 && TP % (kBlock / LPW) == 0, "write passes must tile TP");
+  static_assert(BS % LPW == 0 && TP % (BS / LPW) == 0, "write passes must tile TP");
   __shared__ TO tile[TL][TP + 1];
   const uint32_t id = blockIdx.x;
   const uint32_t bq = fd_div(ta.tilesL, id);
@@ -351,7 +373,7 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
   {
     const int ll = (t % LPW) * VO;
     const uint64_t l = l0 + ll;
-    for (int pp = t / LPW; pp < TP; pp += kBlock / LPW) {
+    for (int pp = t / LPW; pp < TP; pp += BS / LPW) {
       const uint64_t p = p0 + pp;
       if (p >= ta.P) break;
       TO* dst = cb + int64_t(p) * ta.out_sP + int64_t(l);
@@ -371,27 +393,31 @@ __global__ __launch_bounds__(kBlock) void k_unary_transpose(const TI* __restrict
 
 // Launches the tiled transpose with tile (PL lanes along P) x TL; the tile is narrowed along P
 // (and lengthened along L, same LDS bytes) when P is small, so that no tile is mostly empty.
-template <class F, class TO, class TI, int PL, int TL>
+template <class F, class TO, class TI, int PL, int BS, int ROWS>
 bool launch_transpose_tiles(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, bool nts, hipStream_t st, F f) {
   constexpr uint64_t TP = tr_tp<TI, PL>();
+  constexpr int TL = tr_tl<TO, TI, PL, BS, ROWS>();
   const uint64_t tL = (ta.L + TL - 1) / TL, tP = (ta.P + TP - 1) / TP;
   if (tL * tP * nb >= (uint64_t(1) << 31)) return false;
   ta.tilesL = make_fastdiv(uint32_t(tL));
   ta.tilesP = make_fastdiv(uint32_t(tP));
   with_store_policy(nts, [&](auto NT) {
-    k_unary_transpose<F, TO, TI, PL, TL, NT.value><<<dim3(unsigned(tL * tP * nb)), kBlock, 0, st>>>(a, c, ta, f);
+    k_unary_transpose<F, TO, TI, PL, TL, BS, NT.value><<<dim3(unsigned(tL * tP * nb)), BS, 0, st>>>(a, c, ta, f);
   });
   return true;
 }
 
 template <class F, class TO, class TI>
 bool launch_transpose(const TI* a, TO* c, const TransposeArgs& ta, uint64_t nb, bool nts, hipStream_t st, F f) {
-  // LDS per tile: TL x (PL*VI + 1) elements of TO; 32 lanes x 64 rows is 33 KB for f32
+  // LDS per tile: TL x (PL*VI + 1) elements of TO (tr_tl); 32 lanes x 128 rows is 66 KB for f32
   if (ta.P * 4 <= uint64_t(tr_tp<TI, 32>()))
-    return launch_transpose_tiles<F, TO, TI, 8, 256>(a, c, ta, nb, nts, st, f);
+    return launch_transpose_tiles<F, TO, TI, 8, 1024, 256>(a, c, ta, nb, nts, st, f);
   if (ta.P * 2 <= uint64_t(tr_tp<TI, 32>()))
-    return launch_transpose_tiles<F, TO, TI, 16, 128>(a, c, ta, nb, nts, st, f);
-  return launch_transpose_tiles<F, TO, TI, 32, 64>(a, c, ta, nb, nts, st, f);
+    return launch_transpose_tiles<F, TO, TI, 16, 1024, 128>(a, c, ta, nb, nts, st, f);
+  if constexpr (tr_moves_only<F>::value)
+    return launch_transpose_tiles<F, TO, TI, 32, 1024, 128>(a, c, ta, nb, nts, st, f);
+  else
+    return launch_transpose_tiles<F, TO, TI, 32, 512, 64>(a, c, ta, nb, nts, st, f);
 }
 
 // ---------------------------------------------------------------------------------------------

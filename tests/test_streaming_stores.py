@@ -29,7 +29,7 @@ REQUIRED = {
         "k_binary_flat_mixedILi2ELb1ENS_4AddFEdld",  # C3 i64 + f64 -> f64
         "k_binary_rowpiecesILi4ELi2ELb1ENS_4AddFEff",  # C2 broadcast add
         "k_binary_rowsILi4ELi4ELb1ENS_4AddFEff",
-        "k_unary_transposeINS_9IdentityFEiiLi32ELi64ELb1E",  # contiguous X^T f32
+        "k_unary_transposeINS_9IdentityFEiiLi32ELi128ELi1024ELb1E",  # contiguous X^T f32
         "k_unary_rowsILi4ELi4ELb1ENS_9IdentityFEii",  # flip
         "k_unary_flatILi2ELi1ELb1ENS_5CastFIf12musapy_c64_t",  # f32 -> c64
     ],
