@@ -225,12 +225,15 @@ __global__ __launch_bounds__(kFlatBlockBinary) void k_binary_flat_mixed(const TA
 
 // ---------------------------------------------------------------------------------------------
 // row pieces: long output rows (broadcast operands, or operands whose outer strides do not
-// merge).  A block writes U consecutive pieces of kBlock*VEC elements of one row, so neighbouring
-// blocks write neighbouring memory: on MI355X this measured 21.1-21.3 us for C2's
-// (4096,1)+(8192,) against 23.0-23.3 us for column tiles that walk 8 rows each, whose blocks write
-// 4 KB pieces 32 KB apart, and a plain write stream of random data takes 20.7 us.  A lane loads
-// its U items of both operands first (an operand that is row-invariant or one value per row hits
-// the cache), then computes and stores them.
+// merge).  A block writes U consecutive pieces of kPieceBlock*VEC elements of one row, so
+// neighbouring blocks write neighbouring memory (column tiles that walk 8 rows each, whose blocks
+// write 4 KB pieces 32 KB apart, measured 23.0-23.3 us for C2's (4096,1)+(8192,) against 21.1-21.3
+// us).  A lane loads its U items of both operands first (an operand that is row-invariant or one
+// value per row hits the cache), then computes and stores them.  Block shape, measured on MI355X
+// for C2 with streaming stores (kernel time): 512 lanes x 2 pieces 22.4 us, 256 x 2 23.4, 128 x 2
+// 22.7, 1024 x 2 24.8, 256 x 4 23.8, one piece per block 27.5.
+constexpr int kPieceBlock = 512;  // lanes per row-pieces block
+constexpr int kPieces = 2;        // consecutive pieces per block
 struct RowPieceArgs {
   RowIndexer<3> ix;   // outer dims: [0] out, [1] a, [2] b strides
   uint32_t L;         // row length (innermost output dim)
@@ -239,7 +242,7 @@ struct RowPieceArgs {
 };
 
 template <int VEC, int U, bool NTS, class F, class T, class TO = T>
-__global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa, In<T> b, int64_t sb,
+__global__ __launch_bounds__(kPieceBlock) void k_binary_rowpieces(In<T> a, int64_t sa, In<T> b, int64_t sb,
                                                              TO* __restrict__ c, RowPieceArgs ra, F f) {
   const uint32_t row = fd_div(ra.groups, blockIdx.x);
   const uint32_t g = blockIdx.x - row * ra.groups.d;
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa
   T xa[U][VEC], xb[U][VEC];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t col = ((g * U + u) * kBlock + threadIdx.x) * VEC;
+    const uint32_t col = ((g * U + u) * kPieceBlock + threadIdx.x) * VEC;
     if (col >= ra.L) break;
     const bool full = ra.aligned || col + VEC <= ra.L;
     load_item<VEC, T>(a.p + off[1], a.mode, sa, col, ra.L, full && ra.aligned, a.nt, xa[u]);
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_rowpieces(In<T> a, int64_t sa
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t col = ((g * U + u) * kBlock + threadIdx.x) * VEC;
+    const uint32_t col = ((g * U + u) * kPieceBlock + threadIdx.x) * VEC;
     if (col >= ra.L) break;
     TO* cp = c + off[0] + col;
     if (ra.aligned) {
@@ -667,20 +670,20 @@ void launch_binary(const T* a, const T* b, TO* c, int ndim, const size_t* shape,
     uint32_t gpr = (L + V - 1) / V;
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<3> ix = make_row_indexer<3>(p);
-    if (L >= uint32_t(kBlock) * V / 2) {
-      // long rows: blocks of U consecutive row pieces (two pieces measured best for C2)
-      constexpr int U = 2;
+    if (L >= uint32_t(kPieceBlock) * V / 2) {
+      // long rows: blocks of U consecutive row pieces
+      constexpr int U = kPieces;
       RowPieceArgs ra{};
       ra.ix = ix;
       ra.L = L;
       ra.aligned = al;
-      const uint32_t groups = (L + uint32_t(kBlock) * V * U - 1) / (uint32_t(kBlock) * V * U);
+      const uint32_t groups = (L + uint32_t(kPieceBlock) * V * U - 1) / (uint32_t(kPieceBlock) * V * U);
       ra.groups = make_fastdiv(groups);
       const uint64_t blocks = uint64_t(p.numel / L) * groups;
       if (blocks < (uint64_t(1) << 31)) {
         with_store_policy(nts, [&](auto NT) {
-          k_binary_rowpieces<V, U, NT.value, F, T, TO><<<dim3(unsigned(blocks)), kBlock, 0, st>>>(ia, sa, ib, sb, c,
-                                                                                                  ra, f);
+          k_binary_rowpieces<V, U, NT.value, F, T, TO><<<dim3(unsigned(blocks)), kPieceBlock, 0, st>>>(ia, sa, ib, sb,
+                                                                                                       c, ra, f);
         });
         return;
       }
