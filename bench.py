@@ -447,17 +447,19 @@ def cpu_baseline(host):
 def mall_flushed(ms, ops, timer, steps):
     """Each op launched `steps` times, every launch timed alone by HIP events right after 768 MB of
     other traffic (an add over three 256 MB buffers) has replaced what the 256 MB Infinity Cache
-    held: a cold-cache figure beside the back-to-back one.  Returns {name: average ms}."""
+    held: a cold-cache figure beside the back-to-back one.  Returns {name: median ms}: the median,
+    because a single launch timed alone can catch a host-side stall (one such launch under a
+    profiler read 10x the others and turned the average into a figure of the stall)."""
     h = np.full(67_108_864, 1.0, np.float32)
     F = [ms.from_numpy(h) for _ in range(3)]
     del h
     per = {}
     for _, name, fn, _ in ops:
-        tot = 0.0
+        t = []
         for i in range(steps):
             ms.add(F[0], F[1], out=F[2])
-            tot += timer.run([lambda i=i, fn=fn: fn(i)])
-        per[name] = tot / steps
+            t.append(timer.run([lambda i=i, fn=fn: fn(i)]))
+        per[name] = float(np.median(t))
     return per
 
 
@@ -548,7 +550,8 @@ def main():
         "mall_flushed": {"value": round(total_bytes / cold_ms / 1e6, 1), "ms_per_step": round(cold_ms, 5),
                          "ops_ms": {k: round(v, 5) for k, v in cold.items()},
                          "method": "each launch timed alone by HIP events after 768 MB of other traffic "
-                                   "(add over three 256 MB buffers) flushed the Infinity Cache"},
+                                   "(add over three 256 MB buffers) flushed the Infinity Cache; median "
+                                   "per op"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["GBps"], "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": traffic,
                      "algo_bytes": table[dom]["algo_bytes"],
