@@ -14,7 +14,7 @@ import pytest
 
 import musapy_amd as ms
 from oracle import reference as R
-from tests.conftest import assert_bits_equal
+from tests.conftest import assert_bits_equal, ulp_diff_f32
 
 pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(4242)
@@ -89,6 +89,25 @@ def test_contiguous_reference_known_answers():
     assert ms.contiguous(ms.flip(c, 1)).tolist() == [[3.0, 2.0, 1.0], [6.0, 5.0, 4.0]]
     s = ms.array(np.arange(10, dtype=np.float32))[3:7]
     assert ms.contiguous(s).tolist() == [3.0, 4.0, 5.0, 6.0]
+
+
+@pytest.mark.parametrize("shape", [(300, 517), (1030, 70), (70, 1030), (5, 4099), (4099, 5)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_transposed_casts_every_tile_shape(shape):
+    """Casts and unary ops of transposed views go through the LDS tile: 128 rows in 1024 lanes for
+    casts (halved until the tile fits, 32 rows for a 1-byte input widened to 8 bytes), 64 rows in
+    512 lanes for other functors, 8 or 16 lanes along a short P.  Ragged edges on both dims."""
+    casts = [(np.uint8, "f64"), (np.int8, "f32"), (np.int16, "i64"), (np.uint32, "f64"), (np.float32, "f64"),
+             (np.float64, "f32"), (np.int64, "f32"), (np.float32, "c64"), (np.float64, "c128")]
+    for src, dst in casts:
+        x = rand(shape, src) if np.dtype(src).kind in "iu" else RNG.standard_normal(shape).astype(src)
+        got = ms.astype(ms.transpose(ms.from_numpy(x)), dst)
+        assert_bits_equal(got.numpy(), R.cast(x.T, dst), f"{np.dtype(src).name}->{dst} T {shape}", nan_bits=True)
+    x = RNG.uniform(-3, 3, shape).astype(np.float32)
+    e = ms.exp(ms.transpose(ms.from_numpy(x))).numpy()  # expf: within 2 ulp of the oracle, as in C2's test
+    assert e.shape == x.T.shape and ulp_diff_f32(e, R.unary("exp", x.T)).max() <= 2, f"exp T {shape}"
+    h = rand(shape, np.float16)
+    check(ms.contiguous(ms.transpose(ms.from_numpy(h))), R.contiguous(h.T), f"f16 T {shape}")
 
 
 def test_contiguous_large_transpose_and_sizes():
