@@ -141,13 +141,18 @@ __device__ inline void load_item(const T* base, int mode, int64_t s, uint32_t co
   }
 }
 
+// Block of the unary rows kernel: 128 lanes x 4 items.  Measured on MI355X, flip of (8192, 8192)
+// f32 along its rows (kernel time): 86.7-87.0 us, against 90.3 for 256 lanes x 4 items; 512 x 4
+// 89.0, 256 x 2 87.0, 256 x 1 87.8, 1024 x 1 86.5.
+constexpr int kRowsBlock = 128;
+constexpr int kRowsUnroll = 4;
 template <int VEC, int UNROLL, bool NTS, class F, class TO, class TA>
-__global__ __launch_bounds__(kBlock) void k_unary_rows(In<TA> a, int64_t sa, TO* __restrict__ c, RowIndexer<2> ix,
-                                                       FastDiv gpr, uint32_t L, uint32_t items, bool aligned, F f) {
-  const uint32_t first = blockIdx.x * (kBlock * UNROLL) + threadIdx.x;
+__global__ __launch_bounds__(kRowsBlock) void k_unary_rows(In<TA> a, int64_t sa, TO* __restrict__ c, RowIndexer<2> ix,
+                                                           FastDiv gpr, uint32_t L, uint32_t items, bool aligned, F f) {
+  const uint32_t first = blockIdx.x * (kRowsBlock * UNROLL) + threadIdx.x;
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
-    const uint32_t g = first + u * kBlock;
+    const uint32_t g = first + u * kRowsBlock;
     if (g >= items) break;
     const uint32_t row = fd_div(gpr, g);
     const uint32_t col = (g - row * gpr.d) * VEC;
@@ -623,10 +628,10 @@ void launch_unary(const TA* a, TO* c, int ndim, const size_t* shape, const ssize
     uint32_t gpr = (L + V - 1) / V;
     uint32_t items = uint32_t(p.numel / L) * gpr;
     RowIndexer<2> ix = make_row_indexer<2>(p);
-    unsigned grid = (items + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+    unsigned grid = (items + kRowsBlock * kRowsUnroll - 1) / (kRowsBlock * kRowsUnroll);
     with_store_policy(nts, [&](auto NT) {
-      k_unary_rows<V, kUnroll, NT.value, F, TO, TA><<<grid, kBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr), L, items,
-                                                                           al, f);
+      k_unary_rows<V, kRowsUnroll, NT.value, F, TO, TA><<<grid, kRowsBlock, 0, st>>>(ia, sL, c, ix, make_fastdiv(gpr),
+                                                                                   L, items, al, f);
     });
     return;
   }
