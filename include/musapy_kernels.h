@@ -309,17 +309,24 @@ enum { MUSAPY_OP_ADD = 0, MUSAPY_OP_SUB, MUSAPY_OP_MUL, MUSAPY_OP_DIV, MUSAPY_OP
 int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, int b_dtype, void* c, int c_dtype, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
 
 /* ---- single-launch reduction (new; no counterpart in kernels.rs) ----
- * The `_partial_` + `_final_` (`_mid_`) pair in one launch, for a reduction whose axis is
- * unit-stride and is split into `tiles` tiles of at least 16 KB: every (output, tile) block
- * publishes its tile's result into `workspace`, and a combiner block per output, dispatched after
- * them, folds the results in a fixed order -- the result is independent of block timing.  `c`
- * receives the values (the int64 indices for ARGMAX/ARGMIN); `dtype` is the compute dtype (F32,
- * F64 or I64 for every op; C64 and C128 for SUM, PROD and MEAN; MEAN takes a floating or complex
- * dtype).  `workspace` must hold out_size*tiles*W 64-bit words (W = 1 for f32 sum/prod/mean, 2
- * for f64/i64 sum/prod/mean and f32 max/min/arg, 4 for f64/i64 max/min/arg and every complex op),
- * must be zero before the first call, and is left zero by every call; calls that share a
- * workspace must be ordered (one stream).  Returns 0 when launched, -1 when the case is not
- * covered (nothing launched; use the partial + final entry points). */
+ * The `_partial_` + `_final_` (`_mid_`) pair in one launch, for a reduction split into `tiles`
+ * tiles:
+ *  - a unit-stride axis with tiles of at least 16 KB and at most 64 outputs: every (output,
+ *    tile) block publishes its tile's result into `workspace`, and a combiner block per output,
+ *    dispatched after them, folds the results in a fixed order;
+ *  - SUM, PROD and MEAN along a strided axis whose outputs are unit-stride (column reductions):
+ *    the column kernel's (column group, tile) blocks publish their per-column results and count
+ *    themselves per group; the block that completes a group's count folds its tiles in order.
+ * Either way the result is independent of block timing.  `c` receives the values (the int64
+ * indices for ARGMAX/ARGMIN); `dtype` is the compute dtype (F32, F64 or I64 for every op; C64 and
+ * C128 for SUM, PROD and MEAN; MEAN takes a floating or complex dtype).  `workspace` must hold
+ * out_size*tiles*W 64-bit words (W = 1 for f32 sum/prod/mean, 2 for f64/i64 sum/prod/mean and
+ * f32 max/min/arg, 4 for f64/i64 max/min/arg and every complex op; column reductions: groups *
+ * tiles * 64*V*W words, V columns of 16 bytes per lane, plus one 32-bit counter per group, where
+ * groups = out_size / (64*V) rounded up per row of outputs), must be zero before the first call,
+ * and is left zero by every call; calls that share a workspace must be ordered (one stream).
+ * Returns 0 when launched, -1 when the case is not covered, -2 when `workspace` is too small
+ * (nothing launched in either case; use the partial + final entry points). */
 enum { MUSAPY_RED_SUM = 0, MUSAPY_RED_PROD, MUSAPY_RED_MAX, MUSAPY_RED_MIN, MUSAPY_RED_MEAN, MUSAPY_RED_ARGMAX,
        MUSAPY_RED_ARGMIN };
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, void* workspace, size_t workspace_bytes, hipStream_t stream);

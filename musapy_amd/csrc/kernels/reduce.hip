@@ -756,6 +756,112 @@ __global__ __launch_bounds__(BS) void k_reduce_col(const T* __restrict__ a, ColA
 }
 
 // --------------------------------------------------------------------------------------------
+// Column sums, products and means in one launch: the (column group, tile) blocks of k_reduce_col
+// publish wave 0's per-column accumulators (tagged relaxed words, publish.hpp) and count
+// themselves in their group's counter; the block whose increment completes the count folds the
+// group's tiles in tile order, writes the outputs and returns the slots and the counter to zero.
+// Nobody waits but that block, for stores already issued by blocks that have finished (combiner
+// blocks polling from the start of the launch measured slower than partial + final).
+template <class Op, class T, int VEC, int UNROLL, int BS>
+__global__ __launch_bounds__(BS) void k_reduce_col_last(const T* __restrict__ a, ColArgs ca, RedOut<T> out,
+                                                        bool vec_ok, FusedArgs fa, uint32_t* counters) {
+  using A = typename Op::A;
+  static_assert(!Op::kOrdered && sizeof(A) % 4 == 0, "value folds of 32-bit slices");
+  constexpr int W = int(sizeof(A) / 4);
+  __shared__ A part[BS / kWave - 1][kWave * VEC];
+  __shared__ uint32_t s_last;
+  const uint32_t b = blockIdx.x;
+  const uint32_t t = b % ca.tiles;
+  const uint32_t group = b / ca.tiles;  // outer * cgroups + column group
+  const uint32_t cg = group % ca.cgroups;
+  const uint32_t outer = group / ca.cgroups;
+  A acc[VEC];
+  T first[VEC];
+  col_partial<Op, T, VEC, UNROLL, BS>(a, ca, vec_ok, t, cg, outer, part, acc, first);
+  const int lane = threadIdx.x % kWave;
+  const uint64_t c0 = uint64_t(cg) * kWave * VEC + uint64_t(lane) * VEC;
+  auto slot = [&](uint32_t tt, int v) {
+    return fa.slots + ((uint64_t(group) * ca.tiles + tt) * (kWave * VEC) + uint64_t(lane) * VEC + v) * W;
+  };
+  if (threadIdx.x < kWave) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (c0 + v < ca.C) {
+        uint32_t sl[W];
+        __builtin_memcpy(sl, &acc[v], sizeof(A));
+        publish_slices<W>(slot(t, v), sl);
+      }
+  }
+  if (threadIdx.x == 0) s_last = atomicAdd(counters + group, 1u) == ca.tiles - 1 ? 1u : 0u;
+  __syncthreads();
+  if (s_last == 0) return;
+  // The group's last block.  Each round, wave w reads tile t0 + w (every lane its VEC columns, all
+  // words in one round trip) into LDS and clears it; wave 0 then folds the round's tiles in order.
+  constexpr int kWaves = BS / kWave;
+  __shared__ A g[kWaves][kWave * VEC];
+  const int wv = threadIdx.x / kWave;
+  A r[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) r[v] = Op::init();
+  bool ok = true;
+  for (uint32_t t0 = 0; t0 < ca.tiles; t0 += kWaves) {
+    const uint32_t tt = t0 + wv;
+    if (tt < ca.tiles && c0 < ca.C) {
+      uint64_t w[VEC][W];
+      uint32_t pending = 0;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        if (c0 + v < ca.C) pending |= 1u << v;
+      for (uint32_t spins = 0; pending != 0 && spins < fa.spin_limit; ++spins) {  // a limit of 0: no poll
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          if (pending & (1u << v))
+#pragma unroll
+            for (int q = 0; q < W; ++q) w[v][q] = ld_relaxed(slot(tt, v) + q);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          bool ready = true;
+#pragma unroll
+          for (int q = 0; q < W; ++q) ready = ready && (w[v][q] & kTag);
+          if (ready) pending &= ~(1u << v);
+        }
+        if (pending) __builtin_amdgcn_s_sleep(2);
+      }
+      ok = ok && pending == 0;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        if (c0 + v >= ca.C) break;
+        A x = Op::init();
+        if (!(pending & (1u << v))) {
+          uint32_t sl[W];
+#pragma unroll
+          for (int q = 0; q < W; ++q) sl[q] = uint32_t(w[v][q]);
+          __builtin_memcpy(&x, sl, sizeof(A));
+        }
+        g[wv][lane * VEC + v] = x;
+#pragma unroll
+        for (int q = 0; q < W; ++q) st_relaxed(slot(tt, v) + q, 0);
+      }
+    }
+    __syncthreads();
+    if (wv == 0 && c0 < ca.C) {
+      for (int k = 0; k < kWaves && t0 + k < ca.tiles; ++k)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) r[v] = Op::comb(r[v], g[k][lane * VEC + v]);
+    }
+    __syncthreads();
+  }
+  if (__syncthreads_or(ok ? 0 : 1) != 0) {  // a wait ran out: record it and leave the outputs unwritten
+    if (threadIdx.x == 0) atomicOr(fa.fault, kFaultReduceWait);
+  } else if (wv == 0 && c0 < ca.C) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (c0 + v < ca.C) write_result<Op, T, kWriteFinal>(out, uint64_t(outer) * ca.C + c0 + v, r[v], 0);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// --------------------------------------------------------------------------------------------
 // max / min over both axes of a C-contiguous (R, C) array in one launch, with the result the
 // reference's two passes give (reduce_multi, reduction.rs:118-155: axis 0 with keepdims, then
 // axis 1).  Pass 1 keeps, per column, the first row holding the column's extreme, and a column
@@ -1167,6 +1273,42 @@ enum : int { kFusedLaunched = 0, kFusedNotCovered = -1, kFusedNoRoom = -2 };
 template <class Op, class OpF, class T>
 int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, size_t ws_bytes, hipStream_t st);
 
+// Column sums, products and means of `tiles` row tiles in one launch (k_reduce_col_last): the
+// slots hold groups x tiles x (64 * VEC) accumulators, then one 32-bit counter per group.
+template <class Op, class T>
+int launch_reduce_col_last(const T* a, RedOut<T> out, const ReducePlan& p, size_t tiles, void* ws, size_t ws_bytes,
+                           hipStream_t st) {
+  constexpr int V = rvec<T>();
+  constexpr uint64_t W = sizeof(typename Op::A) / 4;
+  if (p.oshape[p.ond - 1] >= (uint64_t(1) << 31) || ceil_div(p.R, uint64_t(tiles)) >= (uint64_t(1) << 31))
+    return kFusedNotCovered;
+  ColArgs ca{};
+  ca.nt = true;
+  ca.ix = out_indexer(p, p.ond - 1);
+  ca.C = p.oshape[p.ond - 1];
+  ca.cgroups = uint32_t(ceil_div(ca.C, uint64_t(kWave) * V));
+  ca.R = p.R;
+  ca.rs = p.rstride;
+  ca.chunk = ceil_div(p.R, uint64_t(tiles));
+  ca.tiles = uint32_t(tiles);
+  bool vec_ok = al16(a) && (ca.C % V == 0) && ((uint64_t(p.rstride < 0 ? -p.rstride : p.rstride) * sizeof(T)) % 16 == 0);
+  for (int d = 0; d < p.ond - 1; ++d)
+    if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) vec_ok = false;
+  const uint64_t groups = (p.out_size / ca.C) * ca.cgroups;
+  const uint64_t blocks = groups * tiles;
+  const uint64_t slot_words = groups * tiles * uint64_t(kWave) * V * W;
+  if (blocks >= (uint64_t(1) << 31)) return kFusedNotCovered;
+  if ((slot_words + ceil_div(groups, uint64_t(2))) * 8 > ws_bytes) return kFusedNoRoom;
+  FusedArgs fa{};
+  fa.slots = static_cast<uint64_t*>(ws);
+  fa.fault = device_fault_word(st);
+  fa.spin_limit = wait_spin_limit();
+  if (fa.fault == nullptr) return kFusedNotCovered;  // a wait that expired could not be reported
+  uint32_t* counters = reinterpret_cast<uint32_t*>(fa.slots + slot_words);
+  k_reduce_col_last<Op, T, V, 4, 512><<<dim3(unsigned(blocks)), 512, 0, st>>>(a, ca, out, vec_ok, fa, counters);
+  return kFusedLaunched;
+}
+
 // The fused single launch for a row-kind reduction split into `tiles` tiles.  kFusedNotCovered
 // (nothing launched) when the shape does not take the 512-lane block path, kFusedNoRoom when the
 // workspace is too small for its slots.
@@ -1174,16 +1316,15 @@ template <class Op, class OpF, class T>
 int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                         size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
   if (out_size == 0 || axis_len == 0 || tiles < 2 || ws == nullptr) return kFusedNotCovered;
-  // Column reductions keep two launches: folding the final into the column kernel through
-  // published slots measured slower ((8192, 8192) f32 axis 0: 48.5 us fused vs 46.3 us for
-  // partial + final at 8 tiles; 63.6 vs 47.0 at 16) -- the cross-block gather costs more than
-  // the final's launch.
-  if (out_size > kFusedMaxOutputs) return kFusedNotCovered;
-  // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
-  if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
   if (!args_ok(ndim, axis)) return kFusedNotCovered;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
+  if constexpr (!Op::kOrdered) {
+    if (p.kind == kColReduce) return launch_reduce_col_last<Op, T>(a, out, p, tiles, ws, ws_bytes, st);
+  }
+  if (out_size > kFusedMaxOutputs) return kFusedNotCovered;
+  // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
+  if (tiles > kFusedMaxTiles) tiles = kFusedMaxTiles;
   if (p.kind != kRowReduce || p.rstride != 1 || !al16(a)) return kFusedNotCovered;
   for (int d = 0; d < p.ond; ++d)
     if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return kFusedNotCovered;

@@ -87,6 +87,18 @@ def test_row_reduction_gives_up_and_recovers():
                        lambda got, what: assert_bits_equal(got, R.reduce(x, "max", 1), what))
 
 
+def test_column_reduction_gives_up_and_recovers():
+    """Column sums and means in one launch: the group's last block finds no tile published."""
+    x = RNG.standard_normal((4096, 2048)).astype(np.float32)
+    for op in ("sum", "mean"):
+        want = R.reduce(x, op, 0)
+
+        def check(got, what, want=want):
+            assert np.all(np.abs(got - want) <= 1e-5 * np.abs(x).sum(axis=0)), what
+
+        _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X, op=op: getattr(ms, op)(X, axis=0), check)
+
+
 def test_row_scan_look_back_gives_up_and_recovers():
     y = RNG.random((4, 100_000))
     want = R.cumsum(y, 1)
