@@ -385,6 +385,29 @@ def test_column_reductions_split_into_row_tiles(kind, dt):
         check_reduce(kind, x, ax)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int64, np.complex64, np.complex128])
+def test_single_launch_column_reductions(dt):
+    """Column sums, means and products in one launch (the last block of each column group folds
+    the group's tiles): ragged column groups, outer dims, back-to-back calls on one workspace, and
+    the same bits run to run."""
+    cases = [((4096, 2048), 0), ((2000, 1030), 0), ((6, 1500, 300), 1), ((8192, 70), 0)]
+    for shape, ax in cases:
+        if dt == np.int64:
+            x = RNG.integers(-1000, 1000, shape).astype(np.int64)
+        elif np.dtype(dt).kind == "c":
+            x = (RNG.standard_normal(shape) + 1j * RNG.standard_normal(shape)).astype(dt)
+        else:
+            x = RNG.standard_normal(shape).astype(dt)
+        X = dev(x)
+        kinds = ("sum", "mean") if dt != np.int64 else ("sum",)
+        for kind in kinds:
+            first = getattr(ms, kind)(X, axis=ax).numpy()
+            check_reduce(kind, x, ax, gpu_x=X)
+            assert_bits_equal(getattr(ms, kind)(X, axis=ax).numpy(), first, f"{kind} {dt.__name__} {shape} rerun")
+    xp = RNG.uniform(0.999, 1.001, (3000, 520)).astype(np.float64 if dt == np.int64 else dt)
+    check_reduce("prod", xp, 0)
+
+
 def test_cumsum_look_back_long_rows():
     """Few long rows take the decoupled look-back over tiles claimed in memory order: a row of
     2^24 f64 is 4096 tiles, so most tiles find their predecessor's prefix beyond the 64-tile window
