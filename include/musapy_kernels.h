@@ -325,8 +325,8 @@ int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, in
  * tiles * 64*V*W words, V columns of 16 bytes per lane, plus one 32-bit counter per group, where
  * groups = out_size / (64*V) rounded up per row of outputs), must be zero before the first call,
  * and is left zero by every call; calls that share a workspace must be ordered (one stream).
- * Returns 0 when launched, -1 when the case is not covered, -2 when `workspace` is too small
- * (nothing launched in either case; use the partial + final entry points). */
+ * Returns 0 when launched, -1 when the case is not covered or `workspace` is too small (nothing
+ * launched; use the partial + final entry points). */
 enum { MUSAPY_RED_SUM = 0, MUSAPY_RED_PROD, MUSAPY_RED_MAX, MUSAPY_RED_MIN, MUSAPY_RED_MEAN, MUSAPY_RED_ARGMAX,
        MUSAPY_RED_ARGMIN };
 int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, void* workspace, size_t workspace_bytes, hipStream_t stream);
@@ -364,8 +364,8 @@ int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_
  * the library (one per GPU, held until the process ends; zeroed by the first call on a device,
  * left zero by every call).  The caller still passes the input and the output.  Returns 0 when
  * launched, -1 when the case is not covered (nothing launched), -2 when its slots need more than
- * the 1 MiB the array holds (out_size * tiles * W words of 8 bytes, W as above; nothing
- * launched, wrapper error 5).  Every call on a GPU shares that GPU's array: calls that overlap
+ * the 1 MiB the array holds (out_size * tiles * W words of 8 bytes, or the column layout's words
+ * and counters, W as above; nothing launched, wrapper error 5).  Every call on a GPU shares that GPU's array: calls that overlap
  * on one GPU (concurrent streams or host threads) race and must be ordered by the caller. */
 int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, hipStream_t stream);
 
