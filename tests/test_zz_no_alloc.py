@@ -106,6 +106,48 @@ def test_noalloc_matches_the_workspace_entry_point(kind, dt):
         check_oracle(kind, got, x)
 
 
+COL_CASES = [(k, d) for d in (np.float32, np.float64, np.int64, np.complex64) for k in ("sum", "mean", "prod")
+             if not (k == "mean" and d == np.int64)]
+
+
+@pytest.mark.parametrize("kind,dt", COL_CASES, ids=[f"{k}-{np.dtype(d).name}" for k, d in COL_CASES])
+def test_noalloc_column_reductions(kind, dt):
+    """Column sums, means and products (axis 0: a strided axis, unit-stride outputs) run in one
+    launch through the static scratch too (the column kernel's last block per group folds): two
+    calls in a row, the second smaller, agree bit for bit with the workspace entry point."""
+    L = lib()
+    for (rows, cols), tiles in (((1024, 2048), 8), ((300, 700), 4)):
+        x = data(kind, dt, (rows, cols))
+        X = ms.from_numpy(x)
+        C1 = ms.from_numpy(np.zeros(cols, dt))
+        C2 = ms.from_numpy(np.zeros(cols, dt))
+        WS = ms.from_numpy(np.zeros(SCRATCH_BYTES // 8, np.uint64))
+        shape = (ctypes.c_size_t * 2)(rows, cols)
+        strides = (ctypes.c_ssize_t * 2)(cols, 1)
+        ms.synchronize()
+        args = (OPS[kind], DT[dt], X.data_ptr)
+        tail = (2, shape, strides, 0, rows, cols, tiles)
+        r1 = L.musapy_reduce_fused_noalloc_v1(*args, C1.data_ptr, *tail, X.stream_ptr)
+        r2 = L.musapy_reduce_fused_v1(*args, C2.data_ptr, *tail, WS.data_ptr, SCRATCH_BYTES, X.stream_ptr)
+        assert (r1, r2) == (0, 0), (kind, dt, rows, cols, tiles, r1, r2)
+        ms.synchronize()
+        assert L.musapy_kernels_take_fault(0) == 0
+        got, ref = C1.numpy(), C2.numpy()
+        what = f"noalloc columns {kind} {np.dtype(dt).name} ({rows}, {cols}) tiles={tiles}"
+        assert_bits_equal(got, ref, what, nan_bits=True)
+        want = R.reduce(x, kind, 0)
+        if want.dtype == np.int64:
+            assert_bits_equal(got, want, what)
+        elif kind == "prod":
+            eps = 1.2e-7 if want.dtype in (np.float32, np.complex64) else 2.3e-16
+            err = np.abs(got.astype(np.complex128) - want) / np.abs(want)
+            assert np.all(err <= 20 * eps * np.sqrt(rows) + 4 * eps), what
+        else:
+            tol = 1e-5 if want.dtype in (np.float32, np.complex64) else 1e-12
+            scale = np.sum(np.abs(x.astype(np.complex128)), axis=0) / (rows if kind == "mean" else 1)
+            assert np.all(np.abs(got.astype(np.complex128) - want) <= tol * scale + 1e-30), what
+
+
 def test_noalloc_refuses_more_slots_than_the_scratch_holds():
     """64 outputs x 513 tiles of f64 max need 64*513*4 = 131,328 words, more than the 131,072 of
     the 1 MiB scratch: refused with -2 and wrapper error 5, nothing launched; the next call,
