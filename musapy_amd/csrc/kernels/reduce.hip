@@ -955,25 +955,29 @@ __global__ __launch_bounds__(BS) void k_reduce_col2d(const T* __restrict__ a, Co
 // (value, column * R + row) (ext_key_f32), is the candidate of that row in column-major order.  Each
 // block publishes its key; the last block folds the R keys with unsigned maxima and reads the
 // winning zero's sign, and x[0][0] when it is NaN, back from the input.  (8192, 8192): kernel
-// 43.9 us, 44.5 us event-timed, against 54.2 us for the column-strip kernel (k_reduce_col2d, still
-// used for f64, i64 and short rows).  Two rows per block measured slower (52 us: the two rows'
+// 43.7-43.8 us, against 54.2 us for the column-strip kernel (k_reduce_col2d, still used for f64,
+// i64 and short rows).  Two rows per block measured slower (52 us: the two rows'
 // registers spill at 8 waves per SIMD).
 // One lane's extreme over row `row` of C f32 elements (C a multiple of 4), in the row kernel's
 // access pattern; with `masked`, elements of columns whose row-0 element (in `a`) is NaN are
 // skipped like NaNs.
+// With `check` (and not `masked`), row 0's values are loaded beside the row's as well, the fold
+// still takes every column, and `nan_seen` tells whether this lane met a NaN in row 0.
 template <class Op, int UNROLL>
 __device__ inline typename Op::A row_extreme(const float* __restrict__ row, const float* __restrict__ a, uint32_t C,
-                                             bool masked) {
+                                             bool masked, bool check, bool& nan_seen) {
   constexpr int VEC = 4;
   constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
   const float qn = qnan<float>();
+  const bool need_h = masked || check;
   typename Op::A acc = Op::init();
+  bool seen = false;
   uint32_t k = uint32_t(threadIdx.x) * VEC;
   for (; k + (UNROLL - 1) * stepk + VEC <= C; k += UNROLL * stepk) {
     Vec<float, VEC> x[UNROLL], h[UNROLL];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) x[u] = vload_nt<float, VEC>(row + k + u * stepk);
-    if (masked) {
+    if (need_h) {
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) h[u] = vload<float, VEC>(a + k + u * stepk);
     }
@@ -982,16 +986,25 @@ __device__ inline typename Op::A row_extreme(const float* __restrict__ row, cons
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) xs[u][v] = (masked && is_nan(h[u].v[v])) ? qn : x[u].v[v];
+      for (int v = 0; v < VEC; ++v) {
+        const bool hn = need_h && is_nan(h[u].v[v]);
+        seen = seen || hn;
+        xs[u][v] = (masked && hn) ? qn : x[u].v[v];
+      }
     acc = Op::template step_chunk<UNROLL, VEC>(acc, xs, k, stepk, 0);
   }
   for (; k < C; k += stepk) {  // the rest of the row, in vectors
     const Vec<float, VEC> xv = vload_nt<float, VEC>(row + k);
     Vec<float, VEC> h{};
-    if (masked) h = vload<float, VEC>(a + k);
+    if (need_h) h = vload<float, VEC>(a + k);
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) acc = Op::step(acc, (masked && is_nan(h.v[v])) ? qn : xv.v[v], int64_t(k + v));
+    for (int v = 0; v < VEC; ++v) {
+      const bool hn = need_h && is_nan(h.v[v]);
+      seen = seen || hn;
+      acc = Op::step(acc, (masked && hn) ? qn : xv.v[v], int64_t(k + v));
+    }
   }
+  nan_seen = seen;
   return acc;
 }
 
@@ -1000,38 +1013,35 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
                                                                    RedOut<float> out, FusedArgs fa) {
   using A = typename Op::A;
   using AF = typename OpF::A;
-  constexpr int VEC = 4;
-  constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
   const uint64_t b = blockIdx.x;
   // published by block 0: 1 + (row 0 holds a NaN), in kFlagCopies copies 256 bytes apart, so that
   // the polls of the other blocks spread over as many memory channels
   constexpr int kFlagCopies = 64;
+  // blocks that check row 0 themselves: one resident generation (256 CUs x 4 blocks of 8 waves)
+  constexpr uint64_t kSelfCheckBlocks = 1024;
   uint64_t* const flag = fa.slots;
   uint64_t* const keys = fa.slots + kFlagCopies * 32;  // one key word per row
   if (b < R) {
     const float* row = a + b * uint64_t(C);
     __shared__ uint32_t s_nanhead;
-    // Which columns count: only those whose row-0 element is not NaN.  Block 0 finds out whether
-    // row 0 holds any NaN and publishes it.  The others fold their row over every column and read
-    // that word at the end (its load is issued first); only when row 0 holds a NaN do they fold
-    // their row again, masking with row 0's values.  Reading row 0 beside every row from the cache
-    // cost 4 us at (8192, 8192); waiting for the word before folding, 2.4 us.
+    // Which columns count: only those whose row-0 element is not NaN.  The blocks of the first
+    // resident generation load row 0 beside their own row (from the cache after the first blocks)
+    // and find out themselves whether it holds a NaN; block 0 publishes that.  Later blocks fold
+    // their row over every column and read the word at the end (its load is issued first).  Only
+    // when row 0 holds a NaN does a block fold its row again, masking with row 0's values.  At
+    // (8192, 8192): the first generation waiting for the word instead cost 0.6 us (44.3-44.5 us
+    // against 43.7-43.8 us), two generations checking 44.4 us, every block checking 4 us more,
+    // and waiting for the word before folding 2.4 us.
+    const bool self = b < kSelfCheckBlocks;
     uint64_t f = 0;
-    if (b == 0) {
-      bool nan_here = false;
-      for (uint32_t j = uint32_t(threadIdx.x) * VEC; j < C; j += stepk) {
-        const Vec<float, VEC> h = vload<float, VEC>(a + j);
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) nan_here = nan_here || is_nan(h.v[v]);
-      }
-      const bool any = __syncthreads_or(nan_here ? 1 : 0) != 0;
-      f = any ? 2 : 1;
-      if (threadIdx.x < kFlagCopies) st_relaxed(flag + threadIdx.x * 32, f);
+    if (!self && threadIdx.x == 0) f = ld_relaxed(flag + (b % kFlagCopies) * 32);
+    bool nan_here = false;
+    A acc = row_extreme<Op, UNROLL>(row, a, C, false, self, nan_here);
+    if (self) {
+      f = __syncthreads_or(nan_here ? 1 : 0) != 0 ? 2 : 1;
+      if (b == 0 && threadIdx.x < kFlagCopies) st_relaxed(flag + threadIdx.x * 32, f);
+      if (threadIdx.x == 0) s_nanhead = uint32_t(f);
     } else if (threadIdx.x == 0) {
-      f = ld_relaxed(flag + (b % kFlagCopies) * 32);
-    }
-    A acc = row_extreme<Op, UNROLL>(row, a, C, false);
-    if (threadIdx.x == 0) {
       for (uint32_t spins = 1; f == 0 && spins < fa.spin_limit; ++spins) {
         __builtin_amdgcn_s_sleep(2);
         f = ld_relaxed(flag + (b % kFlagCopies) * 32);
@@ -1041,7 +1051,7 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
     acc = group_reduce<Op, kRowBS>(acc);  // the row's extreme; its barrier also hands s_nanhead over
     if (s_nanhead != 1) {  // row 0 holds a NaN (or the wait ran out): fold again over the eligible columns
       __syncthreads();     // thread 0 has read the block reduction's partials
-      acc = row_extreme<Op, UNROLL>(row, a, C, true);
+      acc = row_extreme<Op, UNROLL>(row, a, C, true, false, nan_here);
       acc = group_reduce<Op, kRowBS>(acc);  // the row's extreme at its first eligible column
     }
     if (threadIdx.x == 0) {
