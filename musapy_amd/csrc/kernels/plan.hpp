@@ -165,7 +165,7 @@ struct ScanPlan {
 };
 
 inline void plan_scan(ScanPlan& p, int ndim, const size_t* shape, const ssize_t* strides, int axis) {
-  int64_t ostr[kMaxDims];
+  int64_t ostr[kMaxDims] = {};  // callers check 0 <= axis < ndim <= kMaxDims
   {
     int64_t s = 1;
     for (int i = ndim - 1; i >= 0; --i) {

@@ -242,7 +242,7 @@ hipError_t order_after(hipStream_t waiter, hipStream_t target) {
   if (e != hipSuccess) return e;
   e = H().event_record(ev, target);
   if (e == hipSuccess) e = H().stream_wait_event(waiter, ev);
-  H().event_destroy(ev);
+  (void)H().event_destroy(ev);  // the wait holds what it needs; a failed destroy only leaks the event
   return e;
 }
 
@@ -251,14 +251,17 @@ hipError_t release_cached_locked(int device) {
   DevicePool& P = g_pools[device];
   if (P.free.empty()) return hipSuccess;
   int prev = 0;
-  H().get_device(&prev);
+  if (H().get_device(&prev) != hipSuccess) prev = device;
   hipError_t e = H().set_device(device);
   if (e != hipSuccess) return e;
   e = H().device_sync();  // frees were stream-ordered: their work must be done
-  for (auto& kv : P.free) H().free(kv.second.ptr);
+  for (auto& kv : P.free) {
+    const hipError_t fe = H().free(kv.second.ptr);
+    if (e == hipSuccess) e = fe;  // the block leaves the cache either way
+  }
   P.free.clear();
   P.cached_bytes = 0;
-  H().set_device(prev);
+  (void)H().set_device(prev);
   return e;
 }
 
@@ -318,9 +321,10 @@ int mpy_rt_malloc(void** ptr, size_t nbytes, int device, hipStream_t stream) {
   e = injected(MPY_RT_CALL_MALLOC, &code) ? hipError_t(code) : H().malloc(&p, cls);
   if (e == hipErrorOutOfMemory) {
     (void)H().last_error();
-    for (int d = 0; d < kMaxDevices; ++d)
-      if (!g_pools[d].free.empty()) release_cached_locked(d);
-    H().set_device(device);
+    for (int d = 0; d < kMaxDevices; ++d)  // best effort: whatever was released helps the retry
+      if (!g_pools[d].free.empty()) (void)release_cached_locked(d);
+    e = H().set_device(device);
+    if (e != hipSuccess) return rc(e);
     e = injected(MPY_RT_CALL_MALLOC, &code) ? hipError_t(code) : H().malloc(&p, cls);
   }
   if (e != hipSuccess) return rc(e);
