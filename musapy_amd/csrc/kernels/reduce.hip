@@ -1063,6 +1063,12 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
   }
   // combiner: the R row keys
   const float a0 = a[0];
+  // Block 0's flag copies are read here, early (block 0 published them long before this block
+  // started with many rows), and returned to zero below only once seen set: a zero stored without
+  // reading the word could land before block 0's flag store (nothing orders that store before
+  // block 0's key) and leave the flag set for the next launch on this workspace.
+  uint64_t fl = 1;
+  if (threadIdx.x < kFlagCopies) fl = ld_relaxed(flag + threadIdx.x * 32);
   uint64_t key;
   if (fold_keys<PER>(keys, R, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
     AF r = ext_unkey_f32<OpF, int64_t>(key);
@@ -1073,7 +1079,14 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
     if (is_nan(a0)) r = AF{a0, 0};  // column 0 is NaN: it absorbs the second pass
     write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
   }
-  if (threadIdx.x < kFlagCopies) st_relaxed(flag + threadIdx.x * 32, 0);
+  if (threadIdx.x < kFlagCopies) {
+    for (uint32_t spins = 1; fl == 0 && spins < fa.spin_limit; ++spins) {
+      __builtin_amdgcn_s_sleep(2);
+      fl = ld_relaxed(flag + threadIdx.x * 32);
+    }
+    if (fl == 0) atomicOr(fa.fault, kFaultReduceWait);  // reported: the caller zeroes the workspace again
+    st_relaxed(flag + threadIdx.x * 32, 0);
+  }
 }
 
 // --------------------------------------------------------------------------------------------

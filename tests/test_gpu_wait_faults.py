@@ -99,6 +99,20 @@ def test_column_reduction_gives_up_and_recovers():
         _fresh_stream_case(lambda: (ms.from_numpy(x),), lambda X, op=op: getattr(ms, op)(X, axis=0), check)
 
 
+def test_two_axis_reduction_gives_up_and_recovers():
+    """max / min over (0, 1) in one launch (row-keyed kernel, 3000 rows): the combiner finds no row
+    key published, and the row blocks after the first resident generation find no flag from block
+    0 and fold their rows masked instead (always right).  Row 0 with and without a NaN head."""
+    x = RNG.standard_normal((3000, 2048)).astype(np.float32)
+    y = x.copy()
+    y[0, 3] = np.nan  # drops column 3, whatever it holds below
+    y[2999, 3] = 1e30
+    for arr in (x, y):
+        for op in ("max", "min"):
+            _fresh_stream_case(lambda arr=arr: (ms.from_numpy(arr),), lambda X, op=op: getattr(ms, op)(X, axis=(0, 1)),
+                               lambda got, what, arr=arr, op=op: assert_bits_equal(got, R.reduce(arr, op, (0, 1)), what))
+
+
 def test_row_scan_look_back_gives_up_and_recovers():
     y = RNG.random((4, 100_000))
     want = R.cumsum(y, 1)
