@@ -336,7 +336,8 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
  * with its per-tile prefixes in `workspace` instead of the reference's scratch `tmp`: the
  * workspace must be zero before the call and is left zero (each prefix is returned to zero by
  * the tile that reads it), so no clearing launch is needed.  Needs rows * tiles * W 64-bit words
- * (W = 1 for f32, 2 for f64/i64; a tile is 16 KB: 4096 f32 or 2048 f64/i64 elements).  `dtype` is
+ * (W = 1 for f32, 2 for f64/i64; a tile is 64 KB, 16384 f32 or 8192 f64/i64 elements, when a row
+ * holds at least two such tiles, else 16 KB, 4096 f32 or 2048 f64/i64 elements).  `dtype` is
  * MUSAPY_DT_I64, _F32 or _F64.  Returns 0 when launched, -1 when the call does not take that path
  * or the workspace is too small (nothing launched: use musapy_cumsum_*_v3).  Calls that share a
  * workspace must be ordered; after a device wait fault (musapy_kernels_take_fault) zero it

@@ -7,11 +7,12 @@
 //   look-back  the scanned axis is unit-stride and the rows are few, or each row is one tile: a
 //              single pass with a decoupled look-back (Merrill & Garland, "Single-pass Parallel
 //              Prefix Scan with Decoupled Look-back", 2016) over tiles taken in memory order.
-//   chain      unit-stride rows that are many (>= 512) and longer than one tile: 16 KB tiles in
-//              tile-major order over the rows, each waiting only for its row predecessor's
-//              prefix.  On (1024, 65536) f64: 198 us, against 237 us for one block per row walking
-//              it tile by tile (the previous design, whose one-block-per-row access pattern
-//              topped out at the rate of a plain copy in that pattern) and 205 us for 32 KB tiles.
+//   chain      unit-stride rows that are many (>= 512) and longer than one tile: 64 KB tiles
+//              (16 KB for rows shorter than two of them) in tile-major order over the rows, each
+//              waiting only for its row predecessor's prefix.  On (1024, 65536) f64: 180 us, against
+//              188 us with 16 KB tiles and 237 us for one block per row walking it tile by tile (the
+//              previous design, whose one-block-per-row access pattern topped out at the rate of a
+//              plain copy in that pattern).
 //   col        the axis is strided but the innermost other dim is unit-stride: lanes walk
 //              adjacent columns, each carrying a running sum down the axis (coalesced,
 //              sequential order).
@@ -111,8 +112,19 @@ __device__ inline double read_lane(double v, int l) {
 constexpr int kLbBlock = 512;
 constexpr int kVpt = 4;  // 32 KB f64 tiles: measured faster than 16 KB here (fewer look-backs per byte)
 constexpr uint64_t kChainMinRows = 512;  // rows from which the chained scan is used
+// Chained-scan tiles: 1024 lanes x 4 vectors (64 KB, two blocks per CU) for rows of at least two
+// such tiles, else 512 lanes x 2 vectors (16 KB).  The rate falls with the number of rows one XCD
+// streams at once, which in the chain's order is the number of blocks resident on it: at equal
+// bytes in flight per CU, 64 rows of 64 KB tiles beat 128 rows of 32 KB tiles (512 x 4: 196 us
+// against 180 us for (1024, 65536) f64), and 16 KB tiles took 188 us.  One 128 KB tile per CU
+// (1024 x 8) took 205 us: the CU idles at the block's barriers.  Rows of one 64 KB tile or less
+// keep the 16 KB tiles, which give them a chain ((2048, 8192) f64: 48 us against 67 us without).
+constexpr int kChainBigBlock = 1024;
+constexpr int kChainBigVpt = 4;
 constexpr int kChainBlock = 512;
 constexpr int kChainVpt = 2;
+template <class T, int BS, int VPT>
+constexpr uint64_t chain_te() { return uint64_t(BS) * VPT * (16 / sizeof(T)); }
 
 struct LbArgs {
   RowIndexer<2> ix;     // non-axis dims: [0] input strides, [1] output strides
@@ -275,16 +287,17 @@ __global__ __launch_bounds__(kLbBlock) void k_scan_lookback(const T* __restrict_
 // Chained row scan, for many rows of several tiles: tile t of row r is block t * R8 + r (R8 =
 // rows rounded up to a multiple of 8, the blocks past the last row exit at once), so the grid
 // streams tile 0 of every row, then tile 1 of every row, ...  The tile layout and in-tile scan are
-// k_scan_lookback's, with kChainBlock lanes x kChainVpt vectors per tile; a tile's prefix is
+// k_scan_lookback's, with BS lanes x VPT vectors per tile (see kChainBigBlock); a tile's prefix is
 // always P(t) = P(t - 1) + A(t), a fixed association.  Block (r, t) waits only for P(r, t - 1),
 // published by block (r, t - 1): R8 blocks earlier, and on the same XCD (blocks go to the 8 XCDs
 // round-robin by index, and R8 is a multiple of 8), whose workgroups are dispatched in index
 // order -- so the block it waits on is resident or finished, and no atomic tile counter is
 // needed.  The predecessor's prefix is read together with the tile's own loads, and a timing copy
 // that skipped the wait ran as fast: the chain costs nothing measurable at C5, and so does the
-// in-tile scan (a copy in the same block shape took as long).  The tile shape sets the rate:
-// 512 x 2 vectors 198 us, 512 x 4 205 us, 512 x 1 206 us, 256 x 4 215 us, 256 x 2 249 us
-// ((1024, 65536) f64; the smaller tiles lengthen the per-row chain).  A wait is bounded
+// in-tile scan (a copy in the same block shape took as long).  The tile shape sets the rate; with
+// default stores, (1024, 65536) f64: 512 x 2 vectors 198 us, 512 x 4 205 us, 512 x 1 206 us,
+// 256 x 4 215 us, 256 x 2 249 us (the smaller tiles lengthen the per-row chain); with streaming
+// stores see kChainBigBlock.  A wait is bounded
 // (wait_spin_limit polls): when it runs out the tile records kFaultScanWait, takes P = 0 and
 // still publishes, so every block exits.
 struct ChainArgs {
@@ -501,11 +514,18 @@ bool plan_cumsum(ScanShape& sh, const T* a, const T* c, int ndim, const size_t* 
   return true;
 }
 
+// whether the chained scan takes the 64 KB tiles: rows of at least two of them
+template <class T>
+bool chain_big(const ScanShape& sh) {
+  return sh.p.L >= 2 * chain_te<T, kChainBigBlock, kChainBigVpt>();
+}
+
 // tiles of the chained scan per row, 0 when the call does not take it
 template <class T>
 uint64_t chain_tiles(const ScanShape& sh) {
-  constexpr uint64_t CTE = uint64_t(kChainBlock) * kChainVpt * (16 / sizeof(T));
   if (sh.p.kind != kRowScan || sh.p.L <= 16 || sh.p.rows < kChainMinRows) return 0;
+  const uint64_t CTE =
+      chain_big<T>(sh) ? chain_te<T, kChainBigBlock, kChainBigVpt>() : chain_te<T, kChainBlock, kChainVpt>();
   const uint64_t tiles = (sh.p.L + CTE - 1) / CTE;
   return tiles > 1 ? tiles : 0;
 }
@@ -544,8 +564,13 @@ void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_
     unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
     k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
   }
+  const bool big = chain_big<T>(sh);
   with_store_policy(bytes >= kStreamStoreBytes, [&](auto NT) {
-    k_scan_chain<T, kChainBlock, kChainVpt, NT.value><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
+    if (big)
+      k_scan_chain<T, kChainBigBlock, kChainBigVpt, NT.value>
+          <<<dim3(unsigned(R8 * tiles)), kChainBigBlock, 0, st>>>(a, c, ca);
+    else
+      k_scan_chain<T, kChainBlock, kChainVpt, NT.value><<<dim3(unsigned(R8 * tiles)), kChainBlock, 0, st>>>(a, c, ca);
   });
 }
 

@@ -357,7 +357,8 @@ def test_cumsum_workspace_entry_matches_scratch_entry(dt):
     ws_fn.restype = ctypes.c_int
     cs = fn(f"musapy_cumsum_{SFX[dt]}_v3", [P, P, P, I, SZ, SS, I, U, U, P])
     WS = dev_zeros(1 << 17, np.uint64)  # 1 MiB
-    for shape in ((1030, 9000), (520, 4097)):
+    # 16 KB tiles, then the same on a smaller call, then 64 KB tiles (rows of at least two of them)
+    for shape in ((1030, 9000), (520, 4097), (520, 33000)):
         base = RNG.integers(-1000, 1001, shape, dtype=np.int64) if dt == np.int64 else RNG.random(shape).astype(dt)
         B = ms.from_numpy(base)
         x_ptr, sh, st = view_args(B, base, base)

@@ -486,10 +486,10 @@ def test_whole_array_signed_zero_ties(kind):
 
 
 def test_cumsum_chained_rows():
-    """Many rows of several tiles take the chained scan: row counts that are not a multiple of 8
-    (the grid pads the row pitch to one), ragged last tiles, rows that are not 16-byte aligned
-    (a sliced view), int64 exact, floats within the prefix bound of the oracle, and the same bits
-    on every run."""
+    """Many rows of several tiles take the chained scan, in 64 KB tiles (rows of at least two) or
+    16 KB tiles: row counts that are not a multiple of 8 (the grid pads the row pitch to one),
+    ragged last tiles, rows that are not 16-byte aligned (a sliced view), int64 exact, floats
+    within the prefix bound of the oracle, and the same bits on every run."""
     cases = [((515, 70001), np.float64), ((777, 20000), np.int64), ((513, 33333), np.float32),
              ((600, 4097), np.float64), ((1030, 8192), np.float32)]
     for shape, dt in cases:
@@ -506,9 +506,11 @@ def test_cumsum_chained_rows():
             bound = TOL[dt] * np.cumsum(np.abs(x.astype(np.float64)), axis=1) + np.abs(want - exact)
             assert np.all(np.abs(got - want) <= bound), what
         assert_bits_equal(ms.cumsum(X, axis=1).numpy(), got, what + " run-to-run")
-    # a view whose rows start 8 bytes past 16-byte alignment: the element-wise load path
-    base = RNG.random((520, 9001))
-    V = ms.slice(dev(base), [(0, 520, 1), (1, 9001, 1)])
-    got = ms.cumsum(V, axis=1).numpy()
-    want = R.cumsum(base[:, 1:], 1)
-    assert np.all(np.abs(got - want) <= 1e-12 * np.cumsum(np.abs(base[:, 1:]), axis=1)), "unaligned chained rows"
+    # views whose rows start 8 bytes past 16-byte alignment: the element-wise load path, in 16 KB
+    # tiles (rows shorter than two 64 KB tiles) and in 64 KB tiles
+    for cols in (9001, 20001):
+        base = RNG.random((520, cols))
+        V = ms.slice(dev(base), [(0, 520, 1), (1, cols, 1)])
+        got = ms.cumsum(V, axis=1).numpy()
+        want = R.cumsum(base[:, 1:], 1)
+        assert np.all(np.abs(got - want) <= 1e-12 * np.cumsum(np.abs(base[:, 1:]), axis=1)), f"unaligned rows {cols}"

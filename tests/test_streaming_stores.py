@@ -33,7 +33,8 @@ REQUIRED = {
         "k_unary_rowsILi4ELi4ELb1ENS_9IdentityFEii",  # flip
         "k_unary_flatILi2ELi1ELb1ENS_5CastFIf12musapy_c64_t",  # f32 -> c64
     ],
-    "kernels_scan.hip.o": ["k_scan_chainIdLi512ELi2ELb1E"],  # C5 cumsum
+    "kernels_scan.hip.o": ["k_scan_chainIdLi1024ELi4ELb1E",  # C5 cumsum
+                           "k_scan_chainIdLi512ELi2ELb1E"],  # rows of fewer than two 64 KB tiles
 }
 
 
