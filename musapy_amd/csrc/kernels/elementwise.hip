@@ -309,6 +309,10 @@ template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
 //  * 16 or 8 lanes along P (small P): 1024 lanes over 128- or 256-row tiles (the (8192, 128, 64)
 //    permute: 91.0-92.1 us, against 95.1 us over 256 rows).
 // The rows are halved until the tile's LDS fits in 68 KB (wide outputs of narrow inputs).
+// Block order: consecutive blocks take consecutive tiles along L (the output rows), so the blocks
+// in flight write whole output rows.  Groups of 1-16 L tiles taken along P first measured slower
+// for the (8192, 8192) f32 X^T (93.5-97.8 us against 90.0-90.3), level for c128 and exp, and only
+// the (8192, 128, 64) permute gained (89.8-91.0 against 92.4-92.5 us).
 template <class F> struct tr_moves_only : std::false_type {};  // copies and casts
 template <> struct tr_moves_only<IdentityF> : std::true_type {};
 template <class S, class D> struct tr_moves_only<CastF<S, D>> : std::true_type {};
