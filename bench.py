@@ -47,6 +47,32 @@ def parse():
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_step_kernels.md")
 
 
+STEP_TRACE_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "kernel_trace_bench_step.md")
+
+
+def profiled_kernel_us(key):
+    """Average kernel duration (us) of step op `key` in the committed rocprofv3 kernel trace of the
+    default bench (profiles/kernel_trace_bench_step.md), found through the kernel name the
+    traffic summary gives for that key; None when either file lacks it."""
+    name = None
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"\|\s*(add|sum|argmax)\s*\|\s*`([^`]+)`", line)
+                if m and m.group(1) == key:
+                    name = m.group(2)
+        if name is None:
+            return None
+        with open(STEP_TRACE_FILE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 4 and cells[0] == f"`{name}`":
+                    return float(cells[3])  # the first row of that kernel: the step's grid
+    except (OSError, ValueError):
+        return None
+    return None
+
+
 def measured_traffic():
     """HBM bytes per launch of each step kernel, from the committed rocprofv3 --pmc summary:
     FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one pass each) scaled by what the same counters
@@ -64,6 +90,7 @@ def measured_traffic():
 
 
 COPIES = 4  # input copies rotated between launches (4 x the working set >> the 256 MB MALL)
+ROTATED_BYTES = 512 << 20  # per --all row: at least this many bytes of inputs over the rotated copies
 
 
 class Timer:
@@ -126,13 +153,14 @@ def step_ops(ms):
 def all_config_ops(ms, host_legs=False):
     """Every BASELINE config op (for the per-config table), built one at a time.
 
-    Rows are (key, name, build).  build() uploads that op's inputs (3 copies, rotated between
-    launches) and returns (gpu launch of launch index i, algorithmic bytes, cpu leg).  With
+    Rows are (key, name, build).  build() uploads that op's inputs and returns (gpu launch of
+    launch index i, algorithmic bytes, cpu leg).  Each row rotates over K copies of its inputs and
+    keeps its last K outputs alive, with K = max(4, what makes the rotated inputs at least 512 MB),
+    so consecutive launches read and write lines the 256 MB Infinity Cache does not hold.  With
     `host_legs` the BASELINE config rows carry a cpu leg: a function that runs the CPU oracle (the
     single-threaded C restatement of musapy's CPU path) once on the same host inputs and returns
     the algorithmic bytes it covered.  The widened rows carry none.  `key` names the op for
     `--only` (the program profiled under rocprofv3 --pmc)."""
-    K = 3
     R = None
     if host_legs:
         sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -150,6 +178,11 @@ def all_config_ops(ms, host_legs=False):
         if name not in cache:
             cache[name] = make()
         return cache[name]
+
+    def ncopies(*hosts):
+        """Copies to rotate: at least 4, and at least 512 MB of inputs over all copies."""
+        per = sum(h.nbytes for h in hosts)
+        return max(4, -(-ROTATED_BYTES // per))
 
     def a64():
         return get("a64", lambda: np.random.default_rng(0).uniform(-1, 1, 67_108_864).astype(np.float32))
@@ -190,104 +223,123 @@ def all_config_ops(ms, host_legs=False):
                     + 1j * r.standard_normal((16, 1024, 1024), dtype=np.float32)).astype(np.complex64)
         return get("z", mk)
 
-    def up(h):
-        return _copies(ms, h, K)
+    def up(h, k):
+        return _copies(ms, h, k)
 
-    def row(fn, nbytes, cpu=None):
+    def row(fn, nbytes, cpu=None, k=COPIES):
         if fn is None:
             return None, nbytes, cpu
-        # keep the last K results alive, so consecutive launches write K + 1 different output
+        # keep the last k results alive, so consecutive launches write k + 1 different output
         # blocks instead of the one the memory pool would hand back (whose lines the Infinity
         # Cache still holds)
-        ring = [None] * K
+        ring = [None] * k
 
         def g(i):
-            ring[i % K] = fn(i)
+            ring[i % k] = fn(i)
         return g, nbytes, cpu
 
     def b_add64():
-        A, B = up(a64()), up(b64())
-        return row(lambda i: ms.add(A[i % K], B[i % K]), 12 * 67_108_864,
-                   leg(lambda: R.binary("add", a64(), b64()), 12 * 67_108_864))
+        k = ncopies(a64(), b64())
+        A, B = up(a64(), k), up(b64(), k)
+        return row(lambda i: ms.add(A[i % k], B[i % k]), 12 * 67_108_864,
+                   leg(lambda: R.binary("add", a64(), b64()), 12 * 67_108_864), k)
 
     def b_sum64():
-        A = up(a64())
-        return row(lambda i: ms.sum(A[i % K]), 4 * 67_108_864 + 4, leg(lambda: R.reduce(a64(), "sum"), 4 * 67_108_864 + 4))
+        k = ncopies(a64())
+        A = up(a64(), k)
+        return row(lambda i: ms.sum(A[i % k]), 4 * 67_108_864 + 4, leg(lambda: R.reduce(a64(), "sum"), 4 * 67_108_864 + 4),
+                   k)
 
     def b_argmax64():
-        A = up(a64())
-        return row(lambda i: ms.argmax(A[i % K]), 4 * 67_108_864 + 8,
-                   leg(lambda: R.reduce(a64(), "argmax"), 4 * 67_108_864 + 8))
+        k = ncopies(a64())
+        A = up(a64(), k)
+        return row(lambda i: ms.argmax(A[i % k]), 4 * 67_108_864 + 8,
+                   leg(lambda: R.reduce(a64(), "argmax"), 4 * 67_108_864 + 8), k)
 
     def b_sum256():
-        A = up(a256())
-        return row(lambda i: ms.sum(A[i % K]), 4 * 268_435_456 + 4,
-                   leg(lambda: R.reduce(a256(), "sum"), 4 * 268_435_456 + 4))
+        k = ncopies(a256())
+        A = up(a256(), k)
+        return row(lambda i: ms.sum(A[i % k]), 4 * 268_435_456 + 4,
+                   leg(lambda: R.reduce(a256(), "sum"), 4 * 268_435_456 + 4), k)
 
     def b_argmax256():
-        A = up(a256())
-        return row(lambda i: ms.argmax(A[i % K]), 4 * 268_435_456 + 8,
-                   leg(lambda: R.reduce(a256(), "argmax"), 4 * 268_435_456 + 8))
+        k = ncopies(a256())
+        A = up(a256(), k)
+        return row(lambda i: ms.argmax(A[i % k]), 4 * 268_435_456 + 8,
+                   leg(lambda: R.reduce(a256(), "argmax"), 4 * 268_435_456 + 8), k)
 
     def b_bcast():
         ca, cb = c2()
-        CA, CB = up(ca), up(cb)
+        # the broadcast operands are small (48 KB); what streams is the 128 MB output, which the
+        # ring below rotates over k buffers
+        k = ncopies(np.empty(33_554_432, np.float32))
+        CA, CB = up(ca, k), up(cb, k)
         nb = 4 * 33_554_432 + 4 * 4096 + 4 * 8192
-        return row(lambda i: ms.add(CA[i % K], CB[i % K]), nb, leg(lambda: R.binary("add", ca, cb), nb))
+        return row(lambda i: ms.add(CA[i % k], CB[i % k]), nb, leg(lambda: R.binary("add", ca, cb), nb), k)
 
     def b_expT():
         h = get("xe", lambda: np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32))
-        xt = [ms.transpose(c) for c in up(h)]
-        return row(lambda i: ms.exp(xt[i % K]), 8 * 33_554_432, leg(lambda: R.unary("exp", h.T), 8 * 33_554_432))
+        k = ncopies(h)
+        xt = [ms.transpose(c) for c in up(h, k)]
+        return row(lambda i: ms.exp(xt[i % k]), 8 * 33_554_432, leg(lambda: R.unary("exp", h.T), 8 * 33_554_432), k)
 
     def b_c3add():
         i64h, f64h, _, _, _ = c3()
-        I, F = up(i64h), up(f64h)
-        return row(lambda i: ms.add(I[i % K], F[i % K]), 24 * N, leg(lambda: R.binary("add", i64h, f64h), 24 * N))
+        k = ncopies(i64h, f64h)
+        I, F = up(i64h, k), up(f64h, k)
+        return row(lambda i: ms.add(I[i % k], F[i % k]), 24 * N, leg(lambda: R.binary("add", i64h, f64h), 24 * N), k)
 
-    def c3_dev(stage):
+    def c3_dev(stage, k):
         i64h, f64h, _, _, _ = c3()
-        I, F = up(i64h), up(f64h)
-        s_ = [ms.add(I[k], F[k]) for k in range(K)]
+        s_ = []
+        for j in range(k):  # one upload at a time: k copies of the stage, not of every input
+            s_.append(ms.add(ms.from_numpy(i64h), ms.from_numpy(f64h)))
         if stage == "s":
             return s_
-        c_ = [ms.clamp(s_[k], -1.0, 1.0) for k in range(K)]
+        c_ = [ms.clamp(x, -1.0, 1.0) for x in s_]
+        del s_
         if stage == "c":
             return c_
-        return [ms.astype(c_[k], "f32") for k in range(K)]
+        return [ms.astype(x, "f32") for x in c_]
 
     def b_clamp():
-        s_ = c3_dev("s")
         sh = c3()[2]
-        return row(lambda i: ms.clamp(s_[i % K], -1.0, 1.0), 16 * N, leg(lambda: R.clamp(sh, -1.0, 1.0), 16 * N))
+        k = ncopies(sh)
+        s_ = c3_dev("s", k)
+        return row(lambda i: ms.clamp(s_[i % k], -1.0, 1.0), 16 * N, leg(lambda: R.clamp(sh, -1.0, 1.0), 16 * N), k)
 
     def b_f64f32():
-        c_ = c3_dev("c")
         ch = c3()[3]
-        return row(lambda i: ms.astype(c_[i % K], "f32"), 12 * N, leg(lambda: R.cast(ch, "f32"), 12 * N))
+        k = ncopies(ch)
+        c_ = c3_dev("c", k)
+        return row(lambda i: ms.astype(c_[i % k], "f32"), 12 * N, leg(lambda: R.cast(ch, "f32"), 12 * N), k)
 
     def b_bf16():
-        f_ = c3_dev("f")
         fh = c3()[4]
-        return row(lambda i: ms.astype(f_[i % K], "bf16"), 6 * N, leg(lambda: R.cast(fh, "bf16"), 6 * N))
+        k = ncopies(fh)
+        f_ = c3_dev("f", k)
+        return row(lambda i: ms.astype(f_[i % k], "bf16"), 6 * N, leg(lambda: R.cast(fh, "bf16"), 6 * N), k)
 
     def b_f16():
-        f_ = c3_dev("f")
         fh = c3()[4]
-        return row(lambda i: ms.astype(f_[i % K], "f16"), 6 * N, leg(lambda: R.cast(fh, "f16"), 6 * N))
+        k = ncopies(fh)
+        f_ = c3_dev("f", k)
+        return row(lambda i: ms.astype(f_[i % k], "f16"), 6 * N, leg(lambda: R.cast(fh, "f16"), 6 * N), k)
 
     def b_c4(kind, axis, nbytes):
         def b():
-            X = up(xh())
-            return row(lambda i: getattr(ms, kind)(X[i % K], axis=axis), nbytes,
-                       leg(lambda: R.reduce(xh(), kind, axis), nbytes))
+            k = ncopies(xh())
+            X = up(xh(), k)
+            return row(lambda i: getattr(ms, kind)(X[i % k], axis=axis), nbytes,
+                       leg(lambda: R.reduce(xh(), kind, axis), nbytes), k)
         return b
 
     def b_cumsum():
         yh = get("y", lambda: np.random.default_rng(0).random((1024, 65536)))
-        Y = up(yh)
-        return row(lambda i: ms.cumsum(Y[i % K], axis=1), 16 * 1024 * 65536,
-                   leg(lambda: R.cumsum(yh, axis=1), 16 * 1024 * 65536))
+        k = ncopies(yh)
+        Y = up(yh, k)
+        return row(lambda i: ms.cumsum(Y[i % k], axis=1), 16 * 1024 * 65536,
+                   leg(lambda: R.cumsum(yh, axis=1), 16 * 1024 * 65536), k)
 
     def b_cumsum_literal():
         # musapy's literal CPU cumsum re-sums the prefix for every output (O(L^2) per row); rows
@@ -296,59 +348,71 @@ def all_config_ops(ms, host_legs=False):
         return row(None, 16 * 65536, leg(lambda: R.cumsum(yh[:1], axis=1, literal=True), 16 * 65536))
 
     def b_csum():
-        Z = up(zh())
+        k = ncopies(zh())
+        Z = up(zh(), k)
         nb = 8 * 16 * 1024 * 1024 + 128
-        return row(lambda i: ms.sum(Z[i % K], axis=(1, 2)), nb, leg(lambda: R.reduce(zh(), "sum", (1, 2)), nb))
+        return row(lambda i: ms.sum(Z[i % k], axis=(1, 2)), nb, leg(lambda: R.reduce(zh(), "sum", (1, 2)), nb), k)
 
     def b_lt():
-        A, B = up(a64()), up(b64())
-        return row(lambda i: ms.lt(A[i % K], B[i % K]), 9 * 67_108_864)
+        k = ncopies(a64(), b64())
+        A, B = up(a64(), k), up(b64(), k)
+        return row(lambda i: ms.lt(A[i % k], B[i % k]), 9 * 67_108_864, k=k)
 
     def b_eqf64():
-        s_, c_ = c3_dev("s"), c3_dev("c")
-        return row(lambda i: ms.eq(s_[i % K], c_[i % K]), 17 * N)
+        k = ncopies(c3()[2], c3()[3])
+        s_, c_ = c3_dev("s", k), c3_dev("c", k)
+        return row(lambda i: ms.eq(s_[i % k], c_[i % k]), 17 * N, k=k)
 
-    def zpair():
-        Z = up(zh())
-        return Z, [ms.neg(Z[(k + 1) % K]) for k in range(K)]
+    def zpair(k):
+        Z = up(zh(), k)
+        return Z, [ms.neg(Z[(j + 1) % k]) for j in range(k)]
 
     def b_eqc64():
-        Z, Z2 = zpair()
-        return row(lambda i: ms.eq(Z[i % K], Z2[i % K]), 17 * M)
+        k = ncopies(zh(), zh())
+        Z, Z2 = zpair(k)
+        return row(lambda i: ms.eq(Z[i % k], Z2[i % k]), 17 * M, k=k)
 
     def b_cmul(op, dt):
         def b():
-            Z, Z2 = zpair()
+            k = ncopies(zh(), zh())
+            Z, Z2 = zpair(k)
             if dt == "c128":
                 Z, Z2 = [ms.astype(z, "c128") for z in Z], [ms.astype(z, "c128") for z in Z2]
-            return row(lambda i: getattr(ms, op)(Z[i % K], Z2[i % K]), (48 if dt == "c128" else 24) * M)
+            return row(lambda i: getattr(ms, op)(Z[i % k], Z2[i % k]), (48 if dt == "c128" else 24) * M, k=k)
         return b
 
     def b_cabs():
-        Z = up(zh())
-        return row(lambda i: ms.abs(Z[i % K]), 12 * M)
+        k = ncopies(zh())
+        Z = up(zh(), k)
+        return row(lambda i: ms.abs(Z[i % k]), 12 * M, k=k)
 
     def b_f32c64():
-        A = up(a64())
-        return row(lambda i: ms.astype(A[i % K], "c64"), 12 * 67_108_864)
+        k = ncopies(a64())
+        A = up(a64(), k)
+        return row(lambda i: ms.astype(A[i % k], "c64"), 12 * 67_108_864, k=k)
 
     def b_xT():
-        X = up(xh())
-        return row(lambda i: ms.contiguous(ms.transpose(X[i % K])), 8 * n)
+        k = ncopies(xh())
+        X = up(xh(), k)
+        return row(lambda i: ms.contiguous(ms.transpose(X[i % k])), 8 * n, k=k)
 
     def b_perm():
-        P = up(np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32))
-        return row(lambda i: ms.contiguous(ms.permute(P[i % K], [2, 0, 1])), 8 * n)
+        ph = np.random.default_rng(1).standard_normal((8192, 128, 64), dtype=np.float32)
+        k = ncopies(ph)
+        P = up(ph, k)
+        return row(lambda i: ms.contiguous(ms.permute(P[i % k], [2, 0, 1])), 8 * n, k=k)
 
     def b_flip():
-        X = up(xh())
-        return row(lambda i: ms.contiguous(ms.flip(X[i % K], 1)), 8 * n)
+        k = ncopies(xh())
+        X = up(xh(), k)
+        return row(lambda i: ms.contiguous(ms.flip(X[i % k], 1)), 8 * n, k=k)
 
     def b_c128T():
         r = np.random.default_rng(2)
         wm = (r.standard_normal((4096, 4096)) + 1j * r.standard_normal((4096, 4096))).astype(np.complex128)
-        WM = up(wm)
-        return row(lambda i: ms.contiguous(ms.transpose(WM[i % K])), 32 * 4096 * 4096)
+        k = ncopies(wm)
+        WM = up(wm, k)
+        return row(lambda i: ms.contiguous(ms.transpose(WM[i % k])), 32 * 4096 * 4096, k=k)
 
     return [
         ("add64", "C1-64M add f32 67,108,864", b_add64),
@@ -555,9 +619,16 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": table[dom]["GBps"], "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": table[dom]["frac_peak"], "traffic": traffic,
                      "algo_bytes": table[dom]["algo_bytes"],
+                     "frac_basis": "event time: HIP events on the op's stream around the back-to-back launches, "
+                                   "averaged (includes the gap between launches); kernel durations from "
+                                   "rocprofv3 are in profiles/kernel_trace_bench_step.md",
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, os.path.dirname(os.path.abspath(__file__)))
                      if traffic is not None else None},
     }
+    kus = profiled_kernel_us(keys[dom])
+    if kus:
+        line["roofline"]["profiled_kernel_us"] = kus
+        line["roofline"]["frac_by_profiled_kernel_time"] = round(table[dom]["algo_bytes"] / (kus * 1e3) / PEAK_GBS, 4)
     if not args.no_cpu:
         v, sec, sample = cpu_baseline(host)
         line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": 1, "kind": "port",

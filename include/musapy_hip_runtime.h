@@ -76,9 +76,10 @@ void mpy_rt_mem_stats(size_t* live_bytes, size_t* peak_bytes, size_t* num_allocs
 /* Writes `nbytes` of a pattern to `ptr` with a kernel (graph-capture safe, unlike memset). */
 int mpy_rt_fill_u32(void* ptr, uint32_t value, size_t nbytes, hipStream_t stream);
 
-/* The device wait-fault word of the kernel library (musapy_kernels_take_fault), read through the
- * runtime so that tests can inject it: 0, a fault bit set, or -1. */
-int mpy_rt_take_fault(int device);
+/* The wait-fault word of a workspace given to the kernel library (musapy_kernels_take_fault_ws),
+ * read on `stream` through the runtime so that tests can inject it: 0, a fault bit set (the
+ * workspace has been zeroed again), or -1. */
+int mpy_rt_take_fault_ws(void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- test hooks (counterpart of the reference's mock runtime, musa_ffi.rs:154-355) ----
  * mpy_rt_set_backend(MPY_RT_BACKEND_HOST) swaps every HIP call of this layer for a host fake:
@@ -96,7 +97,7 @@ enum {
   MPY_RT_CALL_MEMCPY,     /* host<->device and device copies */
   MPY_RT_CALL_SYNC,       /* stream, device and event synchronizes */
   MPY_RT_CALL_LAUNCH,     /* the launch-error check after a kernel-ABI call */
-  MPY_RT_CALL_FAULT,      /* the device wait-fault word read after a synchronize */
+  MPY_RT_CALL_FAULT,      /* a workspace's wait-fault word read after a synchronize */
   MPY_RT_CALL_EVENT,      /* event create / record / stream wait */
   MPY_RT_CALL_STREAM,     /* stream create */
   MPY_RT_CALL_COUNT

@@ -194,7 +194,11 @@ void musapy_cast_f32_f16_v2(const float* a, uint16_t* c, int ndim, const size_t*
 /* kernels.rs:179 */ void musapy_argmin_f32_v2(const float* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
 /* kernels.rs:180 */ void musapy_argmin_f64_v2(const double* a, int64_t* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
 
-/* ---- cumsum (inclusive scan along one axis; tmp = caller scratch of num_rows*(bpr [+ceil(bpr/256) if bpr>256]) elements, bpr=ceil(axis_len/256), may be NULL when bpr<=1) ---- */
+/* ---- cumsum (inclusive scan along one axis; tmp = caller scratch of num_rows*(bpr [+ceil(bpr/256) if bpr>256]) elements, bpr=ceil(axis_len/256), may be NULL when bpr<=1) ----
+ * A scan whose rows are split into tiles waits on other workgroups; those waits report to the
+ * fault word in the last 8 bytes of that scratch capacity (the workspace rule below), which the
+ * launch zeroes first: read it with musapy_kernels_take_fault_ws(tmp, capacity_bytes, stream)
+ * after synchronizing, before tmp is reused or freed. */
 /* kernels.rs:185 */ void musapy_cumsum_i64_v3(const int64_t* a, int64_t* c, int64_t* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
 /* kernels.rs:186 */ void musapy_cumsum_f32_v3(const float* a, float* c, float* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
 /* kernels.rs:187 */ void musapy_cumsum_f64_v3(const double* a, double* c, double* tmp, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, hipStream_t stream);
@@ -308,7 +312,16 @@ enum {
 enum { MUSAPY_OP_ADD = 0, MUSAPY_OP_SUB, MUSAPY_OP_MUL, MUSAPY_OP_DIV, MUSAPY_OP_POW };
 int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, int b_dtype, void* c, int c_dtype, int ndim, const size_t* shape, const ssize_t* a_strides, const ssize_t* b_strides, hipStream_t stream);
 
-/* ---- single-launch reduction (new; no counterpart in kernels.rs) ----
+/* ---- workspaces of the entry points below (new; no counterpart in kernels.rs) ----
+ * A `workspace` is device memory, 8-byte aligned, of `workspace_bytes` bytes.  Its last 8-byte
+ * word is the workspace's fault word (the first 4 bytes of that word, at offset
+ * (workspace_bytes - 8) rounded down to a multiple of 8); everything before it is payload (slots,
+ * counters, prefixes).  Launches that wait on other workgroups report an expired wait in the
+ * fault word of the workspace they were given, so each caller (stream) reads its own faults
+ * with musapy_kernels_take_fault_ws.  A workspace must be zero before its first use; the
+ * launches leave the payload zero, and the fault word holds faults until they are taken.
+ *
+ * ---- single-launch reduction (new; no counterpart in kernels.rs) ----
  * The `_partial_` + `_final_` (`_mid_`) pair in one launch, for a reduction split into `tiles`
  * tiles:
  *  - a unit-stride axis with tiles of at least 16 KB and at most 64 outputs: every (output,
@@ -319,8 +332,8 @@ int musapy_binary_mixed_v2(int op, const void* a, int a_dtype, const void* b, in
  *    themselves per group; the block that completes a group's count folds its tiles in order.
  * Either way the result is independent of block timing.  `c` receives the values (the int64
  * indices for ARGMAX/ARGMIN); `dtype` is the compute dtype (F32, F64 or I64 for every op; C64 and
- * C128 for SUM, PROD and MEAN; MEAN takes a floating or complex dtype).  `workspace` must hold
- * out_size*tiles*W 64-bit words (W = 1 for f32 sum/prod/mean, 2 for f64/i64 sum/prod/mean and
+ * C128 for SUM, PROD and MEAN; MEAN takes a floating or complex dtype).  The payload of
+ * `workspace` must hold out_size*tiles*W 64-bit words (W = 1 for f32 sum/prod/mean, 2 for f64/i64 sum/prod/mean and
  * f32 max/min/arg, 4 for f64/i64 max/min/arg and every complex op; column reductions: groups *
  * tiles * 64*V*W words, V columns of 16 bytes per lane, plus one 32-bit counter per group, where
  * groups = out_size / (64*V) rounded up per row of outputs), must be zero before the first call,
@@ -334,15 +347,22 @@ int musapy_reduce_fused_v1(int op, int dtype, const void* a, void* c, int ndim, 
 /* ---- cumsum on a zeroed workspace (new; no counterpart in kernels.rs) ----
  * The chained scan of musapy_cumsum_*_v3 for many (>= 512) unit-stride rows of several tiles,
  * with its per-tile prefixes in `workspace` instead of the reference's scratch `tmp`: the
- * workspace must be zero before the call and is left zero (each prefix is returned to zero by
- * the tile that reads it), so no clearing launch is needed.  Needs rows * tiles * W 64-bit words
+ * workspace follows the rule above (zero before the call, payload left zero: each prefix is
+ * returned to zero by the tile that reads it), so no clearing launch is needed.  Its payload
+ * needs rows * tiles * W 64-bit words
  * (W = 1 for f32, 2 for f64/i64; a tile is 64 KB, 16384 f32 or 8192 f64/i64 elements, when a row
  * holds at least two such tiles, else 16 KB, 4096 f32 or 2048 f64/i64 elements).  `dtype` is
  * MUSAPY_DT_I64, _F32 or _F64.  Returns 0 when launched, -1 when the call does not take that path
- * or the workspace is too small (nothing launched: use musapy_cumsum_*_v3).  Calls that share a
- * workspace must be ordered; after a device wait fault (musapy_kernels_take_fault) zero it
- * again. */
+ * or the workspace is too small (nothing launched: use musapy_cumsum_ws_v2 or _v3).  Calls that
+ * share a workspace must be ordered.
+ * musapy_cumsum_ws_v2: every cumsum, with its waits reported to the fault word of `workspace`:
+ * the chained scan on the workspace's payload when it fits (else on `tmp`, cleared first), the
+ * look-back of fewer rows on `tmp` (its claim counter and status words, cleared by the launch),
+ * the sequential scan of a strided axis with neither.  `tmp` may be NULL when the shape takes
+ * no scratch; a `tmp` of the _v3 formula's capacity always suffices.  Returns 0 when launched, -1
+ * when not (wrapper error 1: tmp missing or too small for the path taken; 3 or 4 as for _v3). */
 int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int musapy_cumsum_ws_v2(int dtype, const void* a, void* c, void* tmp, size_t tmp_bytes, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- max / min over both axes of a 2-D array in one launch (new; no counterpart in kernels.rs) ----
  * `a` is a C-contiguous (rows, cols) array of the compute dtype (F32, F64 or I64), and `c`
@@ -350,9 +370,9 @@ int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_
  * passes give (rust/musapy-ops/src/reduction.rs:118-155: axis 0 with keepdims, then axis 1), NaN
  * and signed-zero outcomes included: the first extreme element in column-major order, among the
  * non-NaN elements of the columns whose row-0 element is not NaN, or a[0][0] when that is NaN.
- * `op` is MUSAPY_RED_MAX or MUSAPY_RED_MIN; `workspace` follows musapy_reduce_fused_v1's rules
- * (zero before the first call, left zero).  f32 arrays with cols >= 2048 (a multiple of 4, 16-byte
- * aligned, rows * cols < 2^32 - 1) run as keyed rows and use (2048 + rows) 64-bit words; other
+ * `op` is MUSAPY_RED_MAX or MUSAPY_RED_MIN; `workspace` follows the workspace rule above.  f32
+ * arrays with cols >= 2048 (a multiple of 4, 16-byte aligned, rows * cols < 2^32 - 1) run as keyed
+ * rows and use (2048 + rows) 64-bit words of payload; other
  * shapes use the column tiling and at most 1024 slots of 4 words.  Returns 0 when launched, -1
  * when not covered (more than 1024 groups of 64 16-byte column vectors, or rows >= 2^31): then
  * reduce per axis. */
@@ -361,13 +381,16 @@ int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_
 /* ---- single-launch reduction that allocates nothing (new; no counterpart in kernels.rs) ----
  * For callers that cannot call hipMalloc: code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation.  Same operation, arguments and results as
- * musapy_reduce_fused_v1, without `workspace`: the slots live in a static 1 MiB device array of
- * the library (one per GPU, held until the process ends; zeroed by the first call on a device,
- * left zero by every call).  The caller still passes the input and the output.  Returns 0 when
- * launched, -1 when the case is not covered (nothing launched), -2 when its slots need more than
- * the 1 MiB the array holds (out_size * tiles * W words of 8 bytes, or the column layout's words
- * and counters, W as above; nothing launched, wrapper error 5).  Every call on a GPU shares that GPU's array: calls that overlap
- * on one GPU (concurrent streams or host threads) race and must be ordered by the caller. */
+ * musapy_reduce_fused_v1, without `workspace`: the slots live in a static device array of the
+ * library, 1 MiB of payload plus a 256-byte line ending in its fault word (one per GPU, held until
+ * the process ends, zero when the code object loads, left zero by every call).  The caller still
+ * passes the input and the output.  Returns 0 when launched, -1 when the case is not covered
+ * (nothing launched), -2 when its slots need more than the 1 MiB the array holds (out_size *
+ * tiles * W words of 8 bytes, or the column layout's words and counters, W as above; nothing
+ * launched, wrapper error 5).  Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (concurrent streams or host threads) race and must be ordered by the caller.  Its
+ * expired waits are read with musapy_kernels_take_fault(device); after one, the next call zeroes
+ * the array first, on that call's stream. */
 int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, size_t tiles, hipStream_t stream);
 
 /* ---- wrapper-level error (new; no counterpart in kernels.rs) ----
@@ -381,20 +404,27 @@ int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, in
 int musapy_kernels_take_error(void);
 
 /* ---- device wait faults (new; no counterpart in kernels.rs) ----
- * Two kernels wait for another workgroup's result: the combiner of musapy_reduce_fused_v1 and
- * the look-back of a cumsum whose rows are split into tiles.  Each wait polls a bounded number
- * of times; when that runs out, the kernel records a fault in a per-device word, does not write
- * a result it cannot trust (the reduction skips its output; the scan carries on with a zero
- * prefix), and exits normally.  Results of the work queued since the last check are then
- * invalid, as after a failed kernel (the reference surfaces such errors at stream
- * synchronisation, rust/musapy-core/src/stream.rs:311-377).
- * musapy_kernels_take_fault(device): call after synchronizing the streams whose work it should
- * cover; returns 0 (no fault), a bit set of 1 (a reduction combiner gave up) and 2 (a scan
- * look-back gave up) and clears the word, or -1 when the device cannot be queried.  After a fault,
- * a workspace given to musapy_reduce_fused_v1 may hold stale slots: zero it before reuse.
+ * Three kernels wait for another workgroup's result: the combiners of the single-launch
+ * reductions, the look-back of a cumsum whose rows are split into tiles and the predecessor
+ * wait of the chained scan.  Each wait polls a bounded number of times; when that runs out, the
+ * kernel records a fault in the fault word of the workspace (or scratch) its launch was given,
+ * does not write a result it cannot trust (a reduction skips its output; a scan carries on with
+ * a zero prefix), and exits normally.  Results of the work queued on that workspace since the
+ * last check are then invalid, as after a failed kernel: the reference surfaces such errors at
+ * the synchronisation of the stream that ran the work (rust/musapy-core/src/stream.rs:311-377),
+ * and a workspace here belongs to one stream, so a fault is reported to that stream only.
+ * musapy_kernels_take_fault_ws(workspace, bytes, stream): call after synchronizing `stream` (the
+ * stream the workspace's launches ran on); reads the fault word on `stream` and returns 0 (no
+ * fault), a bit set of 1 (a reduction combiner gave up) and 2 (a scan wait gave up), or -1 on a
+ * HIP error.  A fault also zeroes the whole workspace (payload and word) on `stream` and waits
+ * for that, since a block that published after its combiner gave up may have left a slot
+ * behind; the workspace is then ready for reuse.
+ * musapy_kernels_take_fault(device): the same for the no-alloc scratch of `device` (returns the
+ * bits once; the next no-alloc call zeroes the scratch on its own stream).
  * musapy_kernels_set_spin_limit(polls): sets how many polls a wait makes before it gives up
  * (default 2^24) and returns the previous value; 0 makes every wait give up at once, which lets
  * tests drive the error path while every kernel still exits normally. */
+int musapy_kernels_take_fault_ws(void* workspace, size_t workspace_bytes, hipStream_t stream);
 int musapy_kernels_take_fault(int device);
 uint32_t musapy_kernels_set_spin_limit(uint32_t polls);
 

@@ -29,14 +29,14 @@ from ._core import (  # noqa: F401
     sum, prod, max, min, mean, argmax, argmin, cumsum,
     transpose, flip, index_select, contiguous,
     set_default_device, get_default_device, synchronize, device_count, device_info, mem_stats, empty_cache,
-    Stream, stream, current_stream,
+    Stream, stream, current_stream, set_debug, debug,
 )
 
 __all__ = [
     "Array", "Dtype", "array", "from_numpy", "ones", "add", "sub", "mul", "div", "pow", "sin", "cos", "exp",
     "log", "abs", "sign", "neg", "clamp", "astype", "eq", "ne", "lt", "gt", "le", "ge", "sum", "prod", "max",
     "min", "mean", "argmax", "argmin", "cumsum", "transpose", "permute", "flip", "slice", "index_select",
-    "contiguous", "Stream", "stream", "current_stream", "synchronize", "from_dlpack",
+    "contiguous", "Stream", "stream", "current_stream", "synchronize", "from_dlpack", "set_debug", "debug",
 ]
 
 # dtype constants: Dtype objects that compare equal to their names and aliases

@@ -185,15 +185,30 @@ inline thread_local int g_wrapper_error = 0;
 // ---------------------------------------------------------------------------------------------
 // Bounded device waits.  The kernels that wait for another workgroup's result (the combiner of a
 // single-launch reduction, the look-back of a row scan) poll at most `wait_spin_limit()` times.
-// When that runs out they stop waiting, OR their fault code into the device's fault word, skip
-// or finish their work, and exit normally -- so a grid always drains.  The host reads and clears
-// the word after a synchronize (musapy_kernels_take_fault).
+// When that runs out they stop waiting, OR their fault code into the fault word of the workspace
+// (or scratch) the launch was given, skip or finish their work, and exit normally -- so a grid
+// always drains.  The host reads and clears that word after synchronizing the stream
+// (musapy_kernels_take_fault_ws), so a fault is reported to the stream whose launch gave up.
 enum : uint32_t { kFaultReduceWait = 1u, kFaultScanWait = 2u };
 // polls a bounded wait may make (default 2^24; musapy_kernels_set_spin_limit)
 uint32_t wait_spin_limit();
-// device address of the current device's fault word, nullptr when it cannot be resolved (the
-// first call on a device zeroes it with a kernel on `st`)
-uint32_t* device_fault_word(hipStream_t st);
+
+// A caller's workspace: its last 8-byte word holds the fault word (in its first 4 bytes), and
+// everything before that word is the launch's payload (slots, counters, prefixes).  false when
+// the workspace is missing, not 8-byte aligned, or too small to hold both.
+struct WsSplit {
+  uint64_t* payload;
+  size_t payload_bytes;
+  uint32_t* fault;
+};
+inline bool ws_split(void* ws, size_t bytes, WsSplit& s) {
+  if (ws == nullptr || bytes < 16 || (reinterpret_cast<uintptr_t>(ws) & 7)) return false;
+  const size_t last = (bytes - 8) & ~size_t(7);
+  s.payload = static_cast<uint64_t*>(ws);
+  s.payload_bytes = last;
+  s.fault = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + last);
+  return true;
+}
 
 // The ranks and axes the planners accept: 0 <= ndim <= kMaxDims (the reference's
 // MUSAPY_MAX_NDIM, elementwise.mu:16) and, for a reduction or scan of a non-scalar, 0 <= axis <

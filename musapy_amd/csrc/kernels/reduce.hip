@@ -273,7 +273,7 @@ constexpr size_t kFusedMaxOutputs = 64;
 constexpr size_t kFusedMaxTiles = 2048;  // <= 8 * kRowBS (the largest PER dispatched)
 struct FusedArgs {
   uint64_t* slots;
-  uint32_t* fault;      // the device's fault word (kcommon.hpp)
+  uint32_t* fault;      // the fault word of the launch's workspace (kcommon.hpp)
   uint32_t spin_limit;  // polls the combiner may make before it gives up
 };
 
@@ -1299,12 +1299,12 @@ template <class T> inline RedOut<T> mout(T* c, double cnt) { return RedOut<T>{c,
 enum : int { kFusedLaunched = 0, kFusedNotCovered = -1, kFusedNoRoom = -2 };
 
 template <class Op, class OpF, class T>
-int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, size_t ws_bytes, hipStream_t st);
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, const WsSplit& w, hipStream_t st);
 
 // Column sums, products and means of `tiles` row tiles in one launch (k_reduce_col_last): the
 // slots hold groups x tiles x (64 * VEC) accumulators, then one 32-bit counter per group.
 template <class Op, class T>
-int launch_reduce_col_last(const T* a, RedOut<T> out, const ReducePlan& p, size_t tiles, void* ws, size_t ws_bytes,
+int launch_reduce_col_last(const T* a, RedOut<T> out, const ReducePlan& p, size_t tiles, const WsSplit& w,
                            hipStream_t st) {
   constexpr int V = rvec<T>();
   constexpr uint64_t W = sizeof(typename Op::A) / 4;
@@ -1326,12 +1326,11 @@ int launch_reduce_col_last(const T* a, RedOut<T> out, const ReducePlan& p, size_
   const uint64_t blocks = groups * tiles;
   const uint64_t slot_words = groups * tiles * uint64_t(kWave) * V * W;
   if (blocks >= (uint64_t(1) << 31)) return kFusedNotCovered;
-  if ((slot_words + ceil_div(groups, uint64_t(2))) * 8 > ws_bytes) return kFusedNoRoom;
+  if ((slot_words + ceil_div(groups, uint64_t(2))) * 8 > w.payload_bytes) return kFusedNoRoom;
   FusedArgs fa{};
-  fa.slots = static_cast<uint64_t*>(ws);
-  fa.fault = device_fault_word(st);
+  fa.slots = w.payload;
+  fa.fault = w.fault;
   fa.spin_limit = wait_spin_limit();
-  if (fa.fault == nullptr) return kFusedNotCovered;  // a wait that expired could not be reported
   uint32_t* counters = reinterpret_cast<uint32_t*>(fa.slots + slot_words);
   k_reduce_col_last<Op, T, V, 4, 512><<<dim3(unsigned(blocks)), 512, 0, st>>>(a, ca, out, vec_ok, fa, counters);
   return kFusedLaunched;
@@ -1343,12 +1342,13 @@ int launch_reduce_col_last(const T* a, RedOut<T> out, const ReducePlan& p, size_
 template <class Op, class OpF, class T>
 int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape, const ssize_t* strides, int axis,
                         size_t axis_len, size_t out_size, size_t tiles, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (out_size == 0 || axis_len == 0 || tiles < 2 || ws == nullptr) return kFusedNotCovered;
+  WsSplit w;
+  if (out_size == 0 || axis_len == 0 || tiles < 2 || !ws_split(ws, ws_bytes, w)) return kFusedNotCovered;
   if (!args_ok(ndim, axis)) return kFusedNotCovered;
   ReducePlan p;
   plan_reduce(p, ndim, shape, strides, axis, axis_len, out_size);
   if constexpr (!Op::kOrdered) {
-    if (p.kind == kColReduce) return launch_reduce_col_last<Op, T>(a, out, p, tiles, ws, ws_bytes, st);
+    if (p.kind == kColReduce) return launch_reduce_col_last<Op, T>(a, out, p, tiles, w, st);
   }
   if (out_size > kFusedMaxOutputs) return kFusedNotCovered;
   // 2048 tiles measured best for 64M f32 (a combiner lane then folds 4)
@@ -1358,7 +1358,7 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
     if ((uint64_t(p.ostride[d] < 0 ? -p.ostride[d] : p.ostride[d]) * sizeof(T)) % 16) return kFusedNotCovered;
   // one output over one contiguous run: the interleaved-chunk grid of launch_reduce_all_fused
   if (out_size == 1) {
-    const int r = launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, ws, ws_bytes, st);
+    const int r = launch_reduce_all_fused<Op, OpF, T>(a, out, p.R, w, st);
     if (r != kFusedNotCovered) return r;
   }
   constexpr int V = rvec<T>();
@@ -1367,12 +1367,11 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
   if (uint64_t(out_size) * tiles >= (uint64_t(1) << 31)) return kFusedNotCovered;
   const uint64_t W = sizeof(typename Op::A) / 4;
   const uint64_t words = uint64_t(out_size) * tiles * W;
-  if (words * 8 > ws_bytes) return kFusedNoRoom;
+  if (words * 8 > w.payload_bytes) return kFusedNoRoom;
   FusedArgs fa{};
-  fa.slots = static_cast<uint64_t*>(ws);
-  fa.fault = device_fault_word(st);
+  fa.slots = w.payload;
+  fa.fault = w.fault;
   fa.spin_limit = wait_spin_limit();
-  if (fa.fault == nullptr) return kFusedNotCovered;  // a wait that expired could not be reported
   RowArgs ra{};
   ra.nt = true;
   ra.ix = out_indexer(p, p.ond);
@@ -1406,27 +1405,26 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
 // int64 index, complex sums), whose 8 slots x 4 words would cut the occupancy.
 constexpr uint64_t kAllMaxBlocks = 4096;
 template <class Op, class OpF, class T>
-int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, void* ws, size_t ws_bytes, hipStream_t st) {
+int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, const WsSplit& w, hipStream_t st) {
   constexpr int V = rvec<T>();
   constexpr uint64_t kChunk = uint64_t(kRowBS) * 4 * V;
   constexpr uint64_t W = sizeof(typename OpF::A) / 4;
-  if (n == 0 || ws == nullptr || !al16(a)) return kFusedNotCovered;
+  if (n == 0 || !al16(a)) return kFusedNotCovered;
   const uint64_t nchunks = ceil_div(n, kChunk);
   uint64_t grid = W <= 2 ? ceil_div(nchunks, uint64_t(2)) : nchunks;
   const uint64_t max_grid = W == 1 ? kAllMaxBlocks : W == 2 ? kAllMaxBlocks / 2 : 2 * kRowBS;
   if (grid > max_grid) grid = max_grid;
   if (grid < 2) return kFusedNotCovered;
-  if (grid * W * 8 > ws_bytes) return kFusedNoRoom;
+  if (grid * W * 8 > w.payload_bytes) return kFusedNoRoom;
   FusedArgs fa{};
-  fa.slots = static_cast<uint64_t*>(ws);
-  fa.fault = device_fault_word(st);
+  fa.slots = w.payload;
+  fa.fault = w.fault;
   fa.spin_limit = wait_spin_limit();
-  if (fa.fault == nullptr) return kFusedNotCovered;
   if constexpr (Op::kOrdered && std::is_same_v<T, float>) {
     if (n < 0xffffffffull) {  // one key per block, the grid of one-word accumulators
       uint64_t kg = ceil_div(nchunks, uint64_t(2));
       if (kg > kAllMaxBlocks) kg = kAllMaxBlocks;
-      if (kg >= 2 && kg * 8 <= ws_bytes) {
+      if (kg >= 2 && kg * 8 <= w.payload_bytes) {
         const uint32_t g = uint32_t(kg);
         const uint64_t q = (n / kChunk) / kg;
         const uint32_t r = uint32_t((n / kChunk) % kg);
@@ -1473,17 +1471,17 @@ int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, 
                              hipStream_t st) {
   constexpr int V = rvec<T>();
   constexpr int BS = 256;
-  if (R == 0 || C == 0 || ws == nullptr || R >= (uint64_t(1) << 31) || R * C >= (uint64_t(1) << 62))
+  WsSplit w;
+  if (R == 0 || C == 0 || !ws_split(ws, ws_bytes, w) || R >= (uint64_t(1) << 31) || R * C >= (uint64_t(1) << 62))
     return kFusedNotCovered;
   if constexpr (std::is_same_v<T, float>) {
     // rows of at least one block round: the row-keyed kernel
     if (C >= 2048 && C % 4 == 0 && C < (uint64_t(1) << 31) && R * C < 0xffffffffull && al16(a) &&
-        (64 * 32 + R) * 8 <= ws_bytes) {
+        (64 * 32 + R) * 8 <= w.payload_bytes) {
       FusedArgs fk{};
-      fk.slots = static_cast<uint64_t*>(ws);
-      fk.fault = device_fault_word(st);
+      fk.slots = w.payload;
+      fk.fault = w.fault;
       fk.spin_limit = wait_spin_limit();
-      if (fk.fault == nullptr) return kFusedNotCovered;
       const dim3 g(unsigned(R + 1));
       using OpR = OpExt<float, Op::kMax, false, int32_t>;
       const uint64_t per = ceil_div(R, uint64_t(kRowBS));
@@ -1517,12 +1515,11 @@ int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, 
   const uint32_t nblk = uint32_t(uint64_t(ca.cgroups) * tiles);
   const bool vec_ok = al16(a) && (C % V == 0) && (C * sizeof(T)) % 16 == 0;
   const uint64_t W = sizeof(typename OpF::A) / 4;
-  if (uint64_t(nblk) * W * 8 > ws_bytes) return kFusedNoRoom;
+  if (uint64_t(nblk) * W * 8 > w.payload_bytes) return kFusedNoRoom;
   FusedArgs fa{};
-  fa.slots = static_cast<uint64_t*>(ws);
-  fa.fault = device_fault_word(st);
+  fa.slots = w.payload;
+  fa.fault = w.fault;
   fa.spin_limit = wait_spin_limit();
-  if (fa.fault == nullptr) return kFusedNotCovered;
   const dim3 g(nblk + 1);
   switch (ceil_div(nblk, uint64_t(BS))) {
     case 1: k_reduce_col2d<Op, OpF, T, V, 8, BS, 1><<<g, BS, 0, st>>>(a, ca, nblk, vec_ok, out, fa); break;
@@ -1547,19 +1544,21 @@ template <class T> using OpArgmax64 = OpExt<T, true, true, int64_t>;  // over (v
 template <class T> using OpArgmin64 = OpExt<T, false, true, int64_t>;
 
 // --------------------------------------------------------------------------------------------
-// Device-resident state of the library: the fault word of the bounded waits, and `scratch`, the
-// workspace of the no-alloc single-launch reduction (musapy_reduce_fused_noalloc_v1).  Each GPU
-// the library runs on holds its own copy of both until the process ends.  In host code the
-// names are host-side stand-ins, not device addresses: kernels and copies are only ever given
-// the addresses that hipGetSymbolAddress returns for the current device (DeviceState).
-constexpr size_t kScratchBytes = size_t(1) << 20;  // 1 MiB: out_size * tiles * W <= 131072 words
+// Device-resident state of the library: `scratch`, the workspace of the no-alloc single-launch
+// reduction (musapy_reduce_fused_noalloc_v1).  Its payload is 1 MiB; the 256 bytes after it hold
+// the scratch's fault word (the workspace rule of kcommon.hpp: the last 8-byte word), on a cache
+// line of its own.  Each GPU the library runs on holds its own copy until the process ends,
+// zero-filled by the code object loader (static storage).  In host code the name is a host-side
+// stand-in, not a device address: kernels and copies are only ever given the address that
+// hipGetSymbolAddress returns for the current device (DeviceState).
+constexpr size_t kScratchPayloadBytes = size_t(1) << 20;  // out_size * tiles * W <= 131072 words
+constexpr size_t kScratchBytes = kScratchPayloadBytes + 256;
 static __device__ __align__(256) uint64_t scratch[kScratchBytes / 8];
-static __device__ __align__(256) uint32_t wait_fault;
 
 constexpr int kMaxDevices = 64;
 struct DeviceState {
-  uint64_t* scratch;  // device address of `scratch` on this device
-  uint32_t* fault;    // device address of `wait_fault` on this device
+  uint64_t* scratch;               // device address of `scratch` on this device
+  std::atomic<bool> dirty{false};  // a fault was taken: zero the scratch before its next use
 };
 std::mutex g_state_mu;
 std::atomic<bool> g_state_ready[kMaxDevices];
@@ -1570,11 +1569,18 @@ __global__ void k_zero_words(uint64_t* w, uint64_t n) {
   for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x)
     w[i] = 0;
 }
+// zeroes `bytes` (a multiple of 8) at `p` with a kernel on `st`
+hipError_t zero_on(void* p, size_t bytes, hipStream_t st) {
+  const uint64_t n = bytes / 8;
+  if (n == 0) return hipSuccess;
+  const unsigned g = unsigned(n < 65536 * 256 ? (n + 255) / 256 : 65536);
+  k_zero_words<<<dim3(g), 256, 0, st>>>(static_cast<uint64_t*>(p), n);
+  return hipGetLastError();
+}
 
-// The current device's state, resolved once per device with that device current.  The first call
-// on a device also zeroes both arrays with kernels on `st` (ordered before the caller's work on
-// that stream).  nullptr when a HIP call fails.
-const DeviceState* device_state(hipStream_t st) {
+// The current device's state, its scratch address resolved once per device with that device
+// current; nullptr when a HIP call fails.
+DeviceState* device_state() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     (void)hipGetLastError();
@@ -1584,17 +1590,11 @@ const DeviceState* device_state(hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_state_mu);
   if (!g_state_ready[dev].load(std::memory_order_relaxed)) {
     void* s = nullptr;
-    void* f = nullptr;
-    if (hipGetSymbolAddress(&s, HIP_SYMBOL(scratch)) != hipSuccess || s == nullptr ||
-        hipGetSymbolAddress(&f, HIP_SYMBOL(wait_fault)) != hipSuccess || f == nullptr) {
+    if (hipGetSymbolAddress(&s, HIP_SYMBOL(scratch)) != hipSuccess || s == nullptr) {
       (void)hipGetLastError();
       return nullptr;
     }
     g_state[dev].scratch = static_cast<uint64_t*>(s);
-    g_state[dev].fault = static_cast<uint32_t*>(f);
-    k_zero_words<<<dim3(256), 256, 0, st>>>(g_state[dev].scratch, kScratchBytes / 8);
-    k_zero_words<<<dim3(1), 64, 0, st>>>(reinterpret_cast<uint64_t*>(g_state[dev].fault), 1);
-    if (hipGetLastError() != hipSuccess) return nullptr;
     g_state_ready[dev].store(true, std::memory_order_release);
   }
   return &g_state[dev];
@@ -1602,9 +1602,24 @@ const DeviceState* device_state(hipStream_t st) {
 
 uint32_t wait_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
-uint32_t* device_fault_word(hipStream_t st) {
-  const DeviceState* ds = device_state(st);
-  return ds ? ds->fault : nullptr;
+// Reads the fault word of the workspace [ws, ws + bytes) after the caller's work on `st`; when it
+// is set, zeroes the whole workspace on `st` (a publisher that finished after its combiner gave
+// up may have left a tag in it) and waits for that.  Returns the fault bits, or -1.
+int take_fault_ws(void* ws, size_t bytes, hipStream_t st) {
+  WsSplit w;
+  if (!ws_split(ws, bytes, w)) return -1;
+  uint32_t v = 0;
+  if (hipMemcpyAsync(&v, w.fault, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  if (v == 0) return 0;
+  if (zero_on(ws, w.payload_bytes + 8, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  return int(v);
 }
 
 // one single-launch reduction: kFusedLaunched, kFusedNotCovered or kFusedNoRoom
@@ -1811,12 +1826,17 @@ int musapy_reduce_2d_ordered_v1(int op, int dtype, const void* a, void* c, size_
 }
 
 // The same single launch with the library's static scratch as its workspace (new; no counterpart
-// in kernels.rs): for callers that cannot allocate.  Calls that overlap on one device race.
+// in kernels.rs): for callers that cannot allocate.  Calls that overlap on one device race.  After
+// a fault was taken (musapy_kernels_take_fault) the scratch is zeroed first, on this call's stream.
 int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
                                    const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size,
                                    size_t tiles, hipStream_t st) {
-  const DeviceState* ds = device_state(st);
+  DeviceState* ds = device_state();
   if (ds == nullptr) return -1;
+  if (ds->dirty.load(std::memory_order_acquire)) {
+    if (zero_on(ds->scratch, kScratchBytes, st) != hipSuccess) return -1;
+    ds->dirty.store(false, std::memory_order_release);
+  }
   const int r = fused_dispatch(op, dtype, a, c, RED_PASS, tiles, ds->scratch, kScratchBytes, st);
   if (r == kFusedNoRoom) {
     g_wrapper_error = 5;
@@ -1825,10 +1845,16 @@ int musapy_reduce_fused_noalloc_v1(int op, int dtype, const void* a, void* c, in
   return r == kFusedLaunched ? 0 : -1;
 }
 
-// Returns and clears the device's wait-fault word (kFaultReduceWait | kFaultScanWait), read after
-// the caller has synchronized the streams whose work it covers.  When a fault is found, the
-// static scratch is cleared as well (a publisher that finished after its combiner gave up may
-// have left a tag in it).
+// Returns the fault word of the caller's workspace (kFaultReduceWait | kFaultScanWait), read after
+// the caller's work on `st`; a fault zeroes the workspace on `st` before returning.
+int musapy_kernels_take_fault_ws(void* workspace, size_t workspace_bytes, hipStream_t st) {
+  return take_fault_ws(workspace, workspace_bytes, st);
+}
+
+// Returns and clears the fault word of the device's no-alloc scratch, read after the caller has
+// synchronized the streams whose no-alloc calls it covers.  The scratch itself is zeroed by the
+// next no-alloc call on that device, on that call's stream (a clear issued here would not be
+// ordered with another stream's work).
 int musapy_kernels_take_fault(int device) {
   int prev = 0;
   if (hipGetDevice(&prev) != hipSuccess) return -1;
@@ -1837,20 +1863,18 @@ int musapy_kernels_take_fault(int device) {
     return -1;
   }
   int result = 0;
-  const DeviceState* ds = device_state(nullptr);
+  DeviceState* ds = device_state();
   if (ds == nullptr) {
     result = -1;
-  } else {
+  } else if (!ds->dirty.load(std::memory_order_acquire)) {  // dirty: taken already, no call since
+    WsSplit w;
+    ws_split(ds->scratch, kScratchBytes, w);
     uint32_t v = 0;
-    if (hipMemcpy(&v, ds->fault, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) {
+    if (hipMemcpy(&v, w.fault, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) {
       result = -1;
     } else if (v != 0) {
-      const uint32_t zero = 0;
-      if (hipMemcpy(ds->fault, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess ||
-          hipMemset(ds->scratch, 0, kScratchBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
-        result = -1;
-      else
-        result = int(v);
+      ds->dirty.store(true, std::memory_order_release);
+      result = int(v);
     }
   }
   if (result < 0) (void)hipGetLastError();

@@ -41,9 +41,12 @@ template <> __device__ inline uint64_t from_bits<uint64_t>(uint64_t b) { return 
 
 // Published look-back values (publish.hpp): each status word is written once per launch after
 // k_scan_clear zeroed it, so a reader that sees the tag on every word holds the final value.
-__global__ void k_scan_clear(uint64_t* w, uint64_t n) {
+// `also`, when given, is one more word to zero: the private fault word of a reference-signature
+// call, which sits at the end of its scratch, past the words the scan uses.
+__global__ void k_scan_clear(uint64_t* w, uint64_t n, uint32_t* also) {
   for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x)
     w[i] = 0;
+  if (also != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *also = 0;
 }
 
 // Wave-64 inclusive scan with DPP lane moves (gfx9 DPP: row_shr within rows of 16 lanes, then
@@ -133,7 +136,7 @@ struct LbArgs {
   uint32_t tiles;       // tiles per row
   uint32_t* counter;    // tile claim counter; nullptr when tiles == 1 (no look-back)
   uint64_t* status;     // per tile: W words of A(c), then W words of P(c)
-  uint32_t* fault;      // the device's fault word (kcommon.hpp)
+  uint32_t* fault;      // the fault word of the launch's workspace or scratch (kcommon.hpp)
   uint32_t spin_limit;  // polls a look-back may make
   bool vec;             // 16-byte aligned rows
 };
@@ -308,7 +311,7 @@ struct ChainArgs {
   uint32_t rows;
   uint32_t tiles;       // tiles per row
   uint64_t* prefix;     // per (row, tile): W words of P(row, tile)
-  uint32_t* fault;      // the device's fault word (kcommon.hpp)
+  uint32_t* fault;      // the fault word of the launch's workspace or scratch (kcommon.hpp)
   uint32_t spin_limit;  // polls a wait may make
   bool vec;             // 16-byte aligned rows
   bool nt_load;
@@ -530,11 +533,12 @@ uint64_t chain_tiles(const ScanShape& sh) {
   return tiles > 1 ? tiles : 0;
 }
 
-// The chained scan over `prefix` (rows * tiles * W words).  With `clear` the words are zeroed
-// first; without, they must be zero already (the launch leaves them zero).
+// The chained scan over `prefix` (rows * tiles * W words); an expired wait is reported in
+// `fault`.  With `clear` the words (and `fault` too with `clear_fault`) are zeroed first; without,
+// they must be zero already (the launch leaves them zero).
 template <class T>
 void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_t* prefix, bool clear,
-                  hipStream_t st) {
+                  uint32_t* fault, bool clear_fault, hipStream_t st) {
   const ScanPlan& p = sh.p;
   const uint64_t R8 = (uint64_t(p.rows) + 7) / 8 * 8;
   if (R8 * tiles >= (uint64_t(1) << 31)) {  // block ids
@@ -551,18 +555,14 @@ void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_
   ca.rows = uint32_t(p.rows);
   ca.tiles = uint32_t(tiles);
   ca.prefix = prefix;
-  ca.fault = device_fault_word(st);
+  ca.fault = fault;
   ca.spin_limit = wait_spin_limit();
   ca.vec = sh.vec;
   const uint64_t bytes = uint64_t(p.rows) * p.L * sizeof(T);
   ca.nt_load = bytes >= kStreamLoadBytes;
-  if (ca.fault == nullptr) {  // a wait that ran out could not be reported: take no waits
-    g_wrapper_error = 1;
-    return;
-  }
   if (clear) {
     unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
-    k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words);
+    k_scan_clear<<<cg, 256, 0, st>>>(ca.prefix, words, clear_fault ? fault : nullptr);
   }
   const bool big = chain_big<T>(sh);
   with_store_policy(bytes >= kStreamStoreBytes, [&](auto NT) {
@@ -574,31 +574,43 @@ void launch_chain(const T* a, T* c, const ScanShape& sh, uint64_t tiles, uint64_
   });
 }
 
+// Where a cumsum launch keeps its state: the chained scan's prefixes (`chain`, zero on entry
+// unless `chain_clear`), the look-back's claim counter and status words (`lb`, cleared by the
+// launch), and the fault word its waits report to.  `clear_fault`: the word is private to this
+// call (a reference-signature scratch) and is zeroed with the launch's state; a workspace's word
+// is never zeroed here, since it keeps faults until their owner takes them.
+struct ScanScratch {
+  uint64_t* chain = nullptr;
+  size_t chain_bytes = 0;
+  bool chain_clear = true;
+  uint64_t* lb = nullptr;
+  size_t lb_bytes = 0;
+  uint32_t* fault = nullptr;
+  bool clear_fault = false;
+};
+
+// One cumsum: the chained scan for many rows of several tiles, the look-back for the other row
+// scans of several tiles, the sequential scan otherwise.  Returns false (wrapper error 1, nothing
+// launched) when the path taken needs state that `sc` does not hold.
 template <class T>
-void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
-                   size_t axis_len, size_t out_size, hipStream_t st) {
-  ScanShape sh;
-  if (!plan_cumsum<T>(sh, a, c, ndim, shape, strides, axis, axis_len, out_size)) return;
+bool run_cumsum(const T* a, T* c, const ScanShape& sh, const ScanScratch& sc, hipStream_t st) {
   const ScanPlan& p = sh.p;
-  // tmp capacity per the caller's formula: rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
-  const uint64_t bpr = (p.L + 255) / 256;
-  const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
   const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
   if (p.kind == kRowScan && p.L > 16) {
     // many rows of several tiles: the chained scan, tile-major over the rows
     if (const uint64_t ct = chain_tiles<T>(sh)) {
-      if (tmp == nullptr || uint64_t(p.rows) * ct * W * 8 > cap) {
+      if (sc.chain == nullptr || sc.fault == nullptr || uint64_t(p.rows) * ct * W * 8 > sc.chain_bytes) {
         g_wrapper_error = 1;
-        return;
+        return false;
       }
-      launch_chain<T>(a, c, sh, ct, reinterpret_cast<uint64_t*>(tmp), true, st);
-      return;
+      launch_chain<T>(a, c, sh, ct, sc.chain, sc.chain_clear, sc.fault, sc.clear_fault, st);
+      return true;
     }
     constexpr uint64_t TE = uint64_t(kLbBlock) * kVpt * (16 / sizeof(T));
     const uint64_t tiles = (p.L + TE - 1) / TE;
     if (uint64_t(p.rows) * tiles >= (uint64_t(1) << 32)) {  // tile ids are 32-bit
       g_wrapper_error = 4;
-      return;
+      return false;
     }
     LbArgs sa{};
     sa.ix = sh.ix;
@@ -609,24 +621,20 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
     if (tiles > 1) {
       // word 0: the tile claim counter; then 2 * W status words per tile (aggregate, prefix)
       const uint64_t words = 1 + uint64_t(p.rows) * tiles * 2 * W;
-      if (tmp == nullptr || words * 8 > cap) {
+      if (sc.lb == nullptr || sc.fault == nullptr || words * 8 > sc.lb_bytes) {
         g_wrapper_error = 1;
-        return;
+        return false;
       }
-      uint64_t* w = reinterpret_cast<uint64_t*>(tmp);
+      uint64_t* w = sc.lb;
       sa.counter = reinterpret_cast<uint32_t*>(w);
       sa.status = w + 1;
-      sa.fault = device_fault_word(st);
+      sa.fault = sc.fault;
       sa.spin_limit = wait_spin_limit();
-      if (sa.fault == nullptr) {  // a wait that ran out could not be reported: take no waits
-        g_wrapper_error = 1;
-        return;
-      }
       unsigned cg = unsigned(words < 65536 * 256 ? (words + 255) / 256 : 65536);
-      k_scan_clear<<<cg, 256, 0, st>>>(w, words);
+      k_scan_clear<<<cg, 256, 0, st>>>(w, words, sc.clear_fault ? sc.fault : nullptr);
     }
     k_scan_lookback<T><<<dim3(unsigned(uint64_t(p.rows) * tiles)), kLbBlock, 0, st>>>(a, c, sa);
-    return;
+    return true;
   }
   SeqScanArgs sq{};
   sq.L = p.L;
@@ -642,20 +650,60 @@ void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, cons
   }
   unsigned grid = unsigned((sq.lanes + kSBlock - 1) / kSBlock);
   k_scan_seq<T><<<grid, kSBlock, 0, st>>>(a, c, sq);
+  return true;
 }
 
-// musapy_cumsum_ws_v1: the chained scan on a zeroed workspace, or kFusedNotCovered-style -1
+// The reference-signature entry (musapy_cumsum_*_v3): every piece of state lives in `tmp`, whose
+// capacity is the caller's formula, rows * (bpr [+ ceil(bpr/256) if bpr > 256]) elements
+// (op_builder.rs:3315-3321).  Its last 8-byte word is the fault word (kcommon.hpp), zeroed by
+// the launch that can wait, together with the words it clears.
 template <class T>
-int launch_cumsum_ws(const T* a, T* c, int ndim, const size_t* shape, const ssize_t* strides, int axis,
-                     size_t axis_len, size_t out_size, void* ws, size_t ws_bytes, hipStream_t st) {
+void launch_cumsum(const T* a, T* c, T* tmp, int ndim, const size_t* shape, const ssize_t* strides, int axis,
+                   size_t axis_len, size_t out_size, hipStream_t st) {
   ScanShape sh;
-  if (ws == nullptr || out_size == 0 || axis_len == 0 || !args_ok(ndim, axis)) return -1;
+  if (!plan_cumsum<T>(sh, a, c, ndim, shape, strides, axis, axis_len, out_size)) return;
+  const ScanPlan& p = sh.p;
+  const uint64_t bpr = (p.L + 255) / 256;
+  const uint64_t cap = uint64_t(p.rows) * (bpr + (bpr > 256 ? (bpr + 255) / 256 : 0)) * sizeof(T);
+  ScanScratch sc;
+  WsSplit w;
+  if (ws_split(tmp, cap, w)) {
+    sc.chain = sc.lb = w.payload;
+    sc.chain_bytes = sc.lb_bytes = w.payload_bytes;
+    sc.fault = w.fault;
+    sc.clear_fault = true;  // zeroed by the clear of the prefixes or status words
+  }
+  run_cumsum<T>(a, c, sh, sc, st);
+}
+
+// musapy_cumsum_ws_v2 / _v1: the chained scan on the zeroed payload of `ws` (no clearing launch),
+// the look-back on `tmp` (tmp_bytes of it; may be NULL when the shape does not take it), the
+// fault word in `ws`.  -1 when nothing was launched: `chain_only` and another path, or state
+// missing (wrapper error 1).
+template <class T>
+int launch_cumsum_ws(const T* a, T* c, void* tmp, size_t tmp_bytes, int ndim, const size_t* shape,
+                     const ssize_t* strides, int axis, size_t axis_len, size_t out_size, void* ws, size_t ws_bytes,
+                     bool chain_only, hipStream_t st) {
+  ScanShape sh;
+  WsSplit w;
+  if (!ws_split(ws, ws_bytes, w) || out_size == 0 || axis_len == 0 || !args_ok(ndim, axis)) return -1;
   if (!plan_cumsum<T>(sh, a, c, ndim, shape, strides, axis, axis_len, out_size)) return -1;
   const uint64_t ct = chain_tiles<T>(sh);
   const uint64_t W = sizeof(typename ScanAcc<T>::A) == 4 ? 1 : 2;
-  if (ct == 0 || uint64_t(sh.p.rows) * ct * W * 8 > ws_bytes) return -1;
-  launch_chain<T>(a, c, sh, ct, static_cast<uint64_t*>(ws), false, st);
-  return 0;
+  const bool chain = ct != 0 && uint64_t(sh.p.rows) * ct * W * 8 <= w.payload_bytes;
+  if (chain_only && !chain) return -1;
+  ScanScratch sc;
+  sc.fault = w.fault;
+  if (chain) {
+    sc.chain = w.payload;
+    sc.chain_bytes = w.payload_bytes;
+    sc.chain_clear = false;
+  } else if (tmp != nullptr && (reinterpret_cast<uintptr_t>(tmp) & 7) == 0) {
+    // a chained scan too large for the workspace runs on tmp, cleared first
+    sc.chain = sc.lb = static_cast<uint64_t*>(tmp);
+    sc.chain_bytes = sc.lb_bytes = tmp_bytes & ~size_t(7);
+  }
+  return run_cumsum<T>(a, c, sh, sc, st) ? 0 : -1;
 }
 
 }  // namespace mpy
@@ -680,24 +728,40 @@ void musapy_cumsum_f64_v3(const double* a, double* c, double* tmp, int ndim, con
 
 // The chained scan with a zeroed workspace instead of the reference's scratch (new; no
 // counterpart in kernels.rs): 0 when launched, -1 when the call does not take the chained path
-// or the workspace is too small (nothing launched; use musapy_cumsum_*_v3).
+// or the workspace is too small (nothing launched; use musapy_cumsum_ws_v2 or _v3).
+#define CUMSUM_WS_DISPATCH(TMP, TMPB, CHAIN_ONLY)                                                                   \
+  switch (dtype) {                                                                                                \
+    case MUSAPY_DT_I64:                                                                                           \
+      return launch_cumsum_ws<int64_t>(static_cast<const int64_t*>(a), static_cast<int64_t*>(c), TMP, TMPB, ndim, \
+                                       in_shape, in_strides, axis, axis_len, out_size, workspace,                 \
+                                       workspace_bytes, CHAIN_ONLY, st);                                          \
+    case MUSAPY_DT_F32:                                                                                           \
+      return launch_cumsum_ws<float>(static_cast<const float*>(a), static_cast<float*>(c), TMP, TMPB, ndim,       \
+                                     in_shape, in_strides, axis, axis_len, out_size, workspace, workspace_bytes,  \
+                                     CHAIN_ONLY, st);                                                             \
+    case MUSAPY_DT_F64:                                                                                           \
+      return launch_cumsum_ws<double>(static_cast<const double*>(a), static_cast<double*>(c), TMP, TMPB, ndim,    \
+                                      in_shape, in_strides, axis, axis_len, out_size, workspace, workspace_bytes, \
+                                      CHAIN_ONLY, st);                                                            \
+    default:                                                                                                      \
+      return -1;                                                                                                  \
+  }
 int musapy_cumsum_ws_v1(int dtype, const void* a, void* c, int ndim, const size_t* in_shape,
                         const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size, void* workspace,
                         size_t workspace_bytes, hipStream_t st) {
-  switch (dtype) {
-    case MUSAPY_DT_I64:
-      return launch_cumsum_ws<int64_t>(static_cast<const int64_t*>(a), static_cast<int64_t*>(c), ndim, in_shape,
-                                       in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
-    case MUSAPY_DT_F32:
-      return launch_cumsum_ws<float>(static_cast<const float*>(a), static_cast<float*>(c), ndim, in_shape,
-                                     in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
-    case MUSAPY_DT_F64:
-      return launch_cumsum_ws<double>(static_cast<const double*>(a), static_cast<double*>(c), ndim, in_shape,
-                                      in_strides, axis, axis_len, out_size, workspace, workspace_bytes, st);
-    default:
-      return -1;
-  }
+  CUMSUM_WS_DISPATCH(nullptr, 0, true)
 }
+
+// Any cumsum with its waits reported in the workspace's fault word (new; no counterpart in
+// kernels.rs): the chained scan on the zeroed workspace when it fits, else on `tmp`; the
+// look-back on `tmp`; the sequential scan needs neither.  0 when launched, -1 when not (wrapper
+// error 1: `tmp` missing or too small for the path taken).
+int musapy_cumsum_ws_v2(int dtype, const void* a, void* c, void* tmp, size_t tmp_bytes, int ndim,
+                        const size_t* in_shape, const ssize_t* in_strides, int axis, size_t axis_len, size_t out_size,
+                        void* workspace, size_t workspace_bytes, hipStream_t st) {
+  CUMSUM_WS_DISPATCH(tmp, tmp_bytes, false)
+}
+#undef CUMSUM_WS_DISPATCH
 
 // Returns and clears the calling thread's last wrapper-level error (1 = cumsum scratch missing
 // or too small for the look-back state, 2 = reduction tile above 2^31 elements, 3 = bad rank or

@@ -1,10 +1,15 @@
 // core.cpp -- implementation of the op layer's core types (see core.hpp).
 #include "core.hpp"
 
+#include <strings.h>
+
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <mutex>
+#include <unordered_map>
 
 #include "../../../include/musapy_hip_runtime.h"
 
@@ -214,18 +219,77 @@ void check_launch(const char* label) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// debug mode and op contexts (rust/musapy-core/src/debug.rs:20-100, stream.rs:42-101)
+namespace {
+std::once_flag g_debug_init;
+std::atomic<bool> g_debug{false};
+thread_local bool t_has_frame = false;
+thread_local PythonFrame t_frame;
+
+std::string shape_str(const Shape& s) {
+  std::string r = "(";
+  for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+  return r + (s.size() == 1 ? ",)" : ")");
+}
+}  // namespace
+
+bool is_debug() {
+  std::call_once(g_debug_init, [] {
+    const char* v = std::getenv("MUSAPY_DEBUG");
+    if (v && (std::strcmp(v, "1") == 0 || strcasecmp(v, "true") == 0)) g_debug.store(true, std::memory_order_relaxed);
+  });
+  return g_debug.load(std::memory_order_relaxed);
+}
+void set_debug(bool enabled) {
+  is_debug();  // the environment is read first, so a later first query cannot override this
+  g_debug.store(enabled, std::memory_order_relaxed);
+}
+void set_debug_frame(const PythonFrame* frame) {
+  t_has_frame = frame != nullptr;
+  if (frame) t_frame = *frame;
+}
+bool take_debug_frame(PythonFrame& out) {
+  if (!t_has_frame) return false;
+  t_has_frame = false;
+  out = std::move(t_frame);
+  return true;
+}
+
+std::string OpContext::to_string() const {
+  std::string r = "op '" + op_name + "' on stream " + std::to_string(stream_id);
+  if (!input_shapes.empty()) {
+    r += ", inputs=[";
+    for (size_t i = 0; i < input_shapes.size(); ++i) {
+      r += (i ? ", " : "") + shape_str(input_shapes[i]);
+      if (i < input_dtypes.size()) r += std::string(" ") + dtype_short(input_dtypes[i]);
+    }
+    r += "]";
+  }
+  if (has_frame) r += " at " + frame.filename + ":" + std::to_string(frame.lineno) + " (" + frame.function + ")";
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
 // streams
 namespace {
 std::atomic<uint64_t> g_stream_ids{1};
 std::mutex g_streams_mu;
 std::vector<StreamPtr> g_default_streams;
 thread_local StreamPtr g_current_stream;
+// streams with bounded-wait work queued since their last synchronize, by id (synchronize_device)
+std::mutex g_wait_mu;
+std::unordered_map<uint64_t, std::weak_ptr<Stream>> g_wait_streams;
+void unregister_wait(uint64_t id) {
+  std::lock_guard<std::mutex> lk(g_wait_mu);
+  g_wait_streams.erase(id);
+}
 }  // namespace
 
 Stream::Stream(int device, hipStream_t raw, bool owned)
     : device_(device), raw_(raw), owned_(owned), id_(g_stream_ids.fetch_add(1)) {}
 
 Stream::~Stream() {
+  if (wait_check_) unregister_wait(id_);
   if (workspace_) mpy_rt_free(workspace_, raw_);
   if (owned_ && raw_) mpy_rt_stream_destroy(raw_);
 }
@@ -244,33 +308,90 @@ void* Stream::reduce_workspace() {
   return workspace_;
 }
 
+void Stream::note_bounded_wait() {
+  if (wait_check_) return;
+  wait_check_ = true;
+  std::lock_guard<std::mutex> lk(g_wait_mu);
+  g_wait_streams[id_] = weak_from_this();
+}
+
+void Stream::record_op(OpContext ctx) {
+  std::lock_guard<std::mutex> lk(ops_mu_);
+  pending_ops_.push_back(std::move(ctx));
+}
+size_t Stream::pending_count() const {
+  std::lock_guard<std::mutex> lk(ops_mu_);
+  return pending_ops_.size();
+}
+std::string Stream::oldest_op_string() const {
+  std::lock_guard<std::mutex> lk(ops_mu_);
+  return pending_ops_.empty() ? std::string() : pending_ops_.front().to_string();
+}
+void Stream::clear_pending_ops() {
+  std::lock_guard<std::mutex> lk(ops_mu_);
+  pending_ops_.clear();
+}
+std::string Stream::failed_op_suffix() const {
+  const std::string o = oldest_op_string();
+  return o.empty() ? o : " | failed op: " + o;
+}
+
 void Stream::synchronize() {
   int code = mpy_rt_stream_synchronize(raw_);
   if (code != 0) {
     poisoned_ = true;
-    throw StreamError(std::string("stream synchronize failed: ") + mpy_rt_error_string(code));
+    throw StreamError(std::string("stream synchronize failed: ") + mpy_rt_error_string(code) + failed_op_suffix());
   }
-  if (!wait_check_) return;
-  wait_check_ = false;
-  const int fault = mpy_rt_take_fault(device_);
-  if (fault == 0) return;
-  poisoned_ = true;
-  if (fault < 0) throw StreamError("stream synchronize: the device's wait-fault word could not be read");
-  // A producer that published after its combiner gave up left a tagged slot: start clean.
-  if (workspace_) {
-    int c2 = mpy_rt_fill_u32(workspace_, 0u, kReduceWorkspaceBytes, raw_);
-    if (c2 == 0) c2 = mpy_rt_stream_synchronize(raw_);
-    if (c2 != 0) {
-      mpy_rt_free(workspace_, raw_);  // never reuse slots that may be stale
-      workspace_ = nullptr;
+  if (wait_check_) {
+    wait_check_ = false;
+    unregister_wait(id_);
+    // the workspace holds the fault word of every bounded wait queued on this stream
+    const int fault = workspace_ ? mpy_rt_take_fault_ws(workspace_, kReduceWorkspaceBytes, raw_) : 0;
+    if (fault != 0) {
+      poisoned_ = true;
+      const std::string failed = failed_op_suffix();
+      if (fault < 0) {
+        mpy_rt_free(workspace_, raw_);  // never reuse slots that may be stale
+        workspace_ = nullptr;
+        throw StreamError("stream synchronize: the stream's wait-fault word could not be read" + failed);
+      }
+      std::string what;
+      if (fault & 1) what += "a single-launch reduction's combiner";
+      if (fault & 2) what += std::string(what.empty() ? "" : " and ") + "a cumsum look-back";
+      throw KernelError("device wait expired in " + what + " on stream " + std::to_string(id_) +
+                        ": results of the work queued on this stream since its last synchronize are invalid "
+                        "(stream poisoned)" + failed);
     }
   }
-  std::string what;
-  if (fault & 1) what += "a single-launch reduction's combiner";
-  if (fault & 2) what += std::string(what.empty() ? "" : " and ") + "a cumsum look-back";
-  throw KernelError("device wait expired in " + what +
-                    ": results of the work queued on this stream since its last synchronize are invalid "
-                    "(stream poisoned)");
+  clear_pending_ops();
+}
+
+void synchronize_device(int device) {
+  check_rt(mpy_rt_set_device(device), "set device");
+  check_rt(mpy_rt_device_synchronize(), "device synchronize");
+  std::vector<StreamPtr> pending{default_stream(device)};
+  {
+    std::vector<std::weak_ptr<Stream>> ws;
+    {
+      // the streams are locked outside the mutex: dropping the last reference runs ~Stream,
+      // which takes it
+      std::lock_guard<std::mutex> lk(g_wait_mu);
+      for (auto& kv : g_wait_streams) ws.push_back(kv.second);
+    }
+    for (auto& w : ws) {
+      StreamPtr s = w.lock();
+      if (s && s->device() == device && s != pending.front()) pending.push_back(std::move(s));
+    }
+  }
+  std::exception_ptr first;
+  for (auto& s : pending) {
+    try {
+      s->synchronize();
+    } catch (...) {
+      if (!first) first = std::current_exception();
+    }
+  }
+  if (first) std::rethrow_exception(first);
 }
 
 StreamPtr Stream::create(int device) {

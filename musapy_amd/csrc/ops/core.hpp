@@ -12,8 +12,10 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <deque>
 #include <functional>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -74,8 +76,36 @@ struct Layout {
                 const std::vector<size_t>& step) const;
 };
 
+// ---- debug mode (rust/musapy-core/src/debug.rs:20-100) ----
+// A process-wide flag, off by default, on when MUSAPY_DEBUG is "1" or "true" at first use or after
+// set_debug(true).  While it is on, every op records an OpContext on its output stream, and the
+// Python binding hands the op its caller's frame (set_debug_frame / take_debug_frame).
+bool is_debug();
+void set_debug(bool enabled);
+struct PythonFrame {
+  std::string filename;
+  int lineno = 0;
+  std::string function;
+};
+void set_debug_frame(const PythonFrame* frame);  // nullptr clears it
+bool take_debug_frame(PythonFrame& out);         // the calling thread's frame, consumed
+
+// One op queued on a stream while debug mode is on (stream.rs:42-101): what a failure of that
+// stream is attributed to.
+struct OpContext {
+  std::string op_name;
+  std::vector<Shape> input_shapes;
+  std::vector<int> input_devices;
+  std::vector<Dtype> input_dtypes;
+  Shape output_shape;
+  uint64_t stream_id = 0;
+  bool has_frame = false;
+  PythonFrame frame;
+  std::string to_string() const;  // "op 'add' on stream 3, inputs=[(2, 3), (3,)] at f.py:7 (g)"
+};
+
 // ---- streams (rust/musapy-core/src/stream.rs:154-416) ----
-class Stream {
+class Stream : public std::enable_shared_from_this<Stream> {
  public:
   Stream(int device, hipStream_t raw, bool owned);
   ~Stream();
@@ -88,24 +118,36 @@ class Stream {
   void poison() { poisoned_ = true; }
   // Synchronize (stream.rs:311-377).  A failing synchronize poisons the stream and raises
   // StreamError.  When work with a bounded device wait (note_bounded_wait) was queued since the
-  // last synchronize, the device's wait-fault word is read as well: a wait that ran out poisons
-  // the stream, re-zeroes its reduction workspace and raises KernelError.  As in the reference,
-  // poison is a mark (is_poisoned), not a refusal of later work.
+  // last synchronize, the fault word of this stream's workspace is read as well: a wait that ran
+  // out (in a launch queued on this stream) poisons the stream and raises KernelError; the
+  // library has zeroed the workspace again by then.  As in the reference, poison is a mark
+  // (is_poisoned), not a refusal of later work.  Both errors name the oldest pending op when
+  // debug mode recorded one (stream.rs:392-416); a clean synchronize clears the pending ops.
   void synchronize();
-  // the op layer queued a kernel whose waits can run out (single-launch reduction, row scan)
-  void note_bounded_wait() { wait_check_ = true; }
+  // the op layer queued a kernel whose waits can run out (single-launch reduction, row scan) and
+  // report to this stream's workspace
+  void note_bounded_wait();
   static std::shared_ptr<Stream> create(int device);
   // The priority a caller asked for (stream.rs:154-199).  It is recorded, not applied: every
   // stream of this backend runs at the default priority.
   int priority() const { return priority_; }
   void set_priority(int p) { priority_ = p; }
-  // Scratch for the single-launch reductions queued on this stream: zero-filled once when first
-  // requested, and every such launch leaves it zero again.  Work on one stream is ordered, so
-  // its launches never share it concurrently.
-  static constexpr size_t kReduceWorkspaceBytes = size_t(1) << 20;
+  // Scratch for the single-launch reductions and chained scans queued on this stream: 1 MiB of
+  // slots plus 256 bytes whose last word is the stream's fault word (musapy_kernels.h workspace
+  // rule).  Zero-filled once when first requested; every such launch leaves it zero again.  Work
+  // on one stream is ordered, so its launches never share it concurrently.
+  static constexpr size_t kReduceWorkspaceBytes = (size_t(1) << 20) + 256;
   void* reduce_workspace();
+  // pending op contexts (stream.rs:379-404): recorded in debug mode, cleared by a clean
+  // synchronize
+  void record_op(OpContext ctx);
+  size_t pending_count() const;
+  std::string oldest_op_string() const;  // "" when none
+  void clear_pending_ops();
 
  private:
+  // " | failed op: ..." for an error message, or "" (stream.rs:367-373)
+  std::string failed_op_suffix() const;
   int device_;
   hipStream_t raw_;
   bool owned_;
@@ -114,11 +156,17 @@ class Stream {
   uint64_t id_;
   int priority_ = 0;
   void* workspace_ = nullptr;
+  mutable std::mutex ops_mu_;
+  std::deque<OpContext> pending_ops_;
 };
 using StreamPtr = std::shared_ptr<Stream>;
 
 // per-device default stream of this backend (one non-blocking stream per device)
 StreamPtr default_stream(int device);
+// ms.synchronize(device): waits for the whole device, then synchronizes every live stream of
+// that device with bounded-wait work pending, so a wait that ran out on any of them poisons
+// that stream and raises (the first such error, after all were checked)
+void synchronize_device(int device);
 // the "current stream" override of resolution.rs:184 (nullptr = none)
 StreamPtr current_stream();
 void set_current_stream(StreamPtr s);

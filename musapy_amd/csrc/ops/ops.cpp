@@ -73,6 +73,21 @@ std::vector<size_t> shape_vec(const Shape& s) { return s; }
 
 }  // namespace
 
+void record_op(const char* name, std::initializer_list<const Array*> inputs, const Array& out) {
+  if (!is_debug() || !out.stream) return;
+  OpContext ctx;
+  ctx.op_name = name;
+  for (const Array* x : inputs) {
+    ctx.input_shapes.push_back(x->shape());
+    ctx.input_devices.push_back(x->device);
+    ctx.input_dtypes.push_back(x->dtype);
+  }
+  ctx.output_shape = out.shape();
+  ctx.stream_id = out.stream->id();
+  ctx.has_frame = take_debug_frame(ctx.frame);
+  out.stream->record_op(std::move(ctx));
+}
+
 StreamPtr pick_stream(const Array& a, const Array* out) {
   if (out) return out->stream;
   StreamPtr cur = current_stream();
@@ -845,28 +860,22 @@ Array cumsum_op(const Array& a, std::optional<size_t> axis, const Array* out) {
     const size_t rows = out_size / std::max<size_t>(axis_len, 1);
     const int nd = int(kshape.size());
     s->note_bounded_wait();  // row scans split into tiles wait on their predecessors
-    // many rows: the chained scan on the stream's zeroed workspace (no scratch, no clear launch)
+    // Every cumsum reports its waits to the stream's workspace.  Many rows: the chained scan on
+    // that zeroed workspace (no scratch, no clear launch); fewer rows of several tiles: the
+    // look-back, on scratch of the reference's size (op_builder.rs:3315-3321), taken only when
+    // the first call reports that the path needs it.
     const int dt = ct == Dtype::Int64 ? MUSAPY_DT_I64 : ct == Dtype::Float32 ? MUSAPY_DT_F32 : MUSAPY_DT_F64;
-    if (musapy_cumsum_ws_v1(dt, aw->data_ptr(), r.data_ptr(), nd, kshape.data(), kstrides.data(), kaxis, axis_len,
-                            out_size, s->reduce_workspace(), Stream::kReduceWorkspaceBytes, s->raw()) == 0) {
-      check_launch("cumsum");
-      aw->data->record_read(s);
-      r.data->record_write(s);
-      return r;
-    }
-    const size_t scratch = bpr > 256 ? rows * (bpr + (bpr + 255) / 256) : rows * bpr;
+    void* ws = s->reduce_workspace();
     BufferRef tmp;
-    if (bpr > 1) tmp = Buffer::alloc(scratch * element_size(ct), a.device, s);
-    void* tp = tmp ? tmp->ptr() : nullptr;
-    if (ct == Dtype::Int64)
-      musapy_cumsum_i64_v3((const int64_t*)aw->data_ptr(), (int64_t*)r.data_ptr(), (int64_t*)tp, nd, kshape.data(),
-                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
-    else if (ct == Dtype::Float32)
-      musapy_cumsum_f32_v3((const float*)aw->data_ptr(), (float*)r.data_ptr(), (float*)tp, nd, kshape.data(),
-                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
-    else
-      musapy_cumsum_f64_v3((const double*)aw->data_ptr(), (double*)r.data_ptr(), (double*)tp, nd, kshape.data(),
-                           kstrides.data(), kaxis, axis_len, out_size, s->raw());
+    if (musapy_cumsum_ws_v2(dt, aw->data_ptr(), r.data_ptr(), nullptr, 0, nd, kshape.data(), kstrides.data(), kaxis,
+                            axis_len, out_size, ws, Stream::kReduceWorkspaceBytes, s->raw()) != 0) {
+      (void)musapy_kernels_take_error();  // 1: the path needs scratch (any other error recurs below)
+      const size_t scratch = (bpr > 256 ? rows * (bpr + (bpr + 255) / 256) : rows * bpr) * element_size(ct);
+      tmp = Buffer::alloc(std::max<size_t>(scratch, 8), a.device, s);
+      (void)musapy_cumsum_ws_v2(dt, aw->data_ptr(), r.data_ptr(), tmp->ptr(), tmp->nbytes(), nd, kshape.data(),
+                                kstrides.data(), kaxis, axis_len, out_size, ws, Stream::kReduceWorkspaceBytes,
+                                s->raw());
+    }
     check_launch("cumsum");
   }
   aw->data->record_read(s);

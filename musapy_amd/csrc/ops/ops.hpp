@@ -63,5 +63,10 @@ Array import_dlpack(void* managed, bool versioned);
 // stream resolution used by every Phase A (op_builder.rs:402-405, resolution.rs:184)
 StreamPtr pick_stream(const Array& a, const Array* out);
 
+// Phase C in debug mode (op_builder.rs:507-521): records the op's OpContext (name, the inputs'
+// shapes, devices and dtypes, the output's shape, the caller's Python frame when the binding set
+// one) on the output's stream; nothing when debug mode is off.
+void record_op(const char* name, std::initializer_list<const Array*> inputs, const Array& out);
+
 }  // namespace ops
 }  // namespace mpy

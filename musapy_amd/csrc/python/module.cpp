@@ -131,6 +131,36 @@ std::optional<std::vector<ssize_t>> parse_axes(const py::object& axis, bool& is_
   return v;
 }
 
+// Debug mode (rust/musapy-python/src/ops.rs:104-113): the caller's Python frame, handed to the
+// op layer, which stores it in the op's OpContext.
+void capture_frame() {
+  PyFrameObject* f = PyEval_GetFrame();
+  if (f == nullptr) return;
+  PythonFrame fr;
+  fr.lineno = PyFrame_GetLineNumber(f);
+  PyCodeObject* code = PyFrame_GetCode(f);
+  py::object c = py::reinterpret_steal<py::object>(reinterpret_cast<PyObject*>(code));
+  fr.filename = py::str(c.attr("co_filename"));
+  fr.function = py::str(c.attr("co_name"));
+  set_debug_frame(&fr);
+}
+
+// Runs op `f` and, in debug mode, records its OpContext on the output's stream.
+template <class F>
+Array traced(const char* name, std::initializer_list<const Array*> inputs, F&& f) {
+  if (!is_debug()) return f();
+  capture_frame();
+  try {
+    Array r = f();
+    record_op(name, inputs, r);
+    set_debug_frame(nullptr);
+    return r;
+  } catch (...) {
+    set_debug_frame(nullptr);  // a failed op records nothing
+    throw;
+  }
+}
+
 Array reduce_py(const Array& a, const py::object& axis, bool keepdims, const Array* out, ReduceKernel k) {
   bool none = false;
   auto ax = parse_axes(axis, none);
@@ -268,6 +298,7 @@ PYBIND11_MODULE(_core, m) {
         py::gil_scoped_release nogil;
         s.synchronize();
       })
+      .def_property_readonly("pending_count", &Stream::pending_count)
       .def_property_readonly("priority", &Stream::priority)
       .def_property_readonly("device", [](const Stream& s) { return dev_str(s.device()); })
       .def_property_readonly("id", &Stream::id)
@@ -354,14 +385,18 @@ PYBIND11_MODULE(_core, m) {
       .def("is_contiguous", [](const Array& a) { return a.is_contiguous(); })
       .def("is_0d", [](const Array& a) { return a.ndim() == 0; })
       .def("numpy", [](const Array& a) { return to_numpy(a); })
-      .def("__add__", [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Add); })
-      .def("__sub__", [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Sub); })
-      .def("__mul__", [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Mul); })
-      .def("__truediv__",
-           [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Div); })
-      .def("__pow__", [](const Array& a, const Array& b) { return binary_elementwise(a, b, nullptr, BinaryKernel::Pow); })
-      .def("__neg__", [](const Array& a) { return unary_elementwise(a, nullptr, UnaryKernel::Neg); })
-      .def("__abs__", [](const Array& a) { return unary_elementwise(a, nullptr, UnaryKernel::Abs); })
+#define DBIN(NAME, OP, K)                                                                                      \
+  .def(NAME, [](const Array& a, const Array& b) {                                                              \
+    return traced(OP, {&a, &b}, [&] { return binary_elementwise(a, b, nullptr, K); });                         \
+  })
+      DBIN("__add__", "add", BinaryKernel::Add)
+      DBIN("__sub__", "sub", BinaryKernel::Sub)
+      DBIN("__mul__", "mul", BinaryKernel::Mul)
+      DBIN("__truediv__", "div", BinaryKernel::Div)
+      DBIN("__pow__", "pow", BinaryKernel::Pow)
+#undef DBIN
+      .def("__neg__", [](const Array& a) { return traced("neg", {&a}, [&] { return unary_elementwise(a, nullptr, UnaryKernel::Neg); }); })
+      .def("__abs__", [](const Array& a) { return traced("abs", {&a}, [&] { return unary_elementwise(a, nullptr, UnaryKernel::Abs); }); })
       // comparisons (rust/musapy-python/src/array.rs:174-208): elementwise, bool result
       .def("__eq__", [](const Array& a, const Array& b) { return comparison_elementwise(a, b, nullptr, CompareKernel::Eq); },
            py::is_operator())
@@ -380,7 +415,10 @@ PYBIND11_MODULE(_core, m) {
 
 #define BIN(NAME, K)                                                                                 \
   m.def(                                                                                             \
-      #NAME, [](const Array& a, const Array& b, const Array* out) { return binary_elementwise(a, b, out, K); }, \
+      #NAME,                                                                                         \
+      [](const Array& a, const Array& b, const Array* out) {                                         \
+        return traced(#NAME, {&a, &b}, [&] { return binary_elementwise(a, b, out, K); });            \
+      },                                                                                             \
       py::arg("a"), py::arg("b"), py::arg("out") = nullptr);
   BIN(add, BinaryKernel::Add)
   BIN(sub, BinaryKernel::Sub)
@@ -390,7 +428,10 @@ PYBIND11_MODULE(_core, m) {
 #undef BIN
 #define CMP(NAME, K)                                                                                          \
   m.def(                                                                                                      \
-      #NAME, [](const Array& a, const Array& b, const Array* out) { return comparison_elementwise(a, b, out, K); }, \
+      #NAME,                                                                                                  \
+      [](const Array& a, const Array& b, const Array* out) {                                                  \
+        return traced(#NAME, {&a, &b}, [&] { return comparison_elementwise(a, b, out, K); });                 \
+      },                                                                                                      \
       py::arg("a"), py::arg("b"), py::arg("out") = nullptr);
   CMP(eq, CompareKernel::Eq)
   CMP(ne, CompareKernel::Ne)
@@ -399,9 +440,13 @@ PYBIND11_MODULE(_core, m) {
   CMP(le, CompareKernel::Le)
   CMP(ge, CompareKernel::Ge)
 #undef CMP
-#define UN(NAME, K) \
-  m.def(#NAME, [](const Array& a, const Array* out) { return unary_elementwise(a, out, K); }, py::arg("a"), \
-        py::arg("out") = nullptr);
+#define UN(NAME, K)                                                                                    \
+  m.def(                                                                                               \
+      #NAME,                                                                                           \
+      [](const Array& a, const Array* out) {                                                           \
+        return traced(#NAME, {&a}, [&] { return unary_elementwise(a, out, K); });                      \
+      },                                                                                               \
+      py::arg("a"), py::arg("out") = nullptr);
   UN(sin, UnaryKernel::Sin)
   UN(cos, UnaryKernel::Cos)
   UN(exp, UnaryKernel::Exp)
@@ -410,15 +455,26 @@ PYBIND11_MODULE(_core, m) {
   UN(sign, UnaryKernel::Sign)
   UN(neg, UnaryKernel::Neg)
 #undef UN
-  m.def("clamp", [](const Array& a, double lo, double hi, const Array* out) { return clamp_elementwise(a, lo, hi, out); },
-        py::arg("a"), py::arg("lo"), py::arg("hi"), py::arg("out") = nullptr);
-  m.def("astype", [](const Array& a, const py::object& d, const Array* out) { return astype_op(a, dtype_arg(d), out); },
-        py::arg("a"), py::arg("dtype"), py::arg("out") = nullptr);
+  m.def(
+      "clamp",
+      [](const Array& a, double lo, double hi, const Array* out) {
+        return traced("clamp", {&a}, [&] { return clamp_elementwise(a, lo, hi, out); });
+      },
+      py::arg("a"), py::arg("lo"), py::arg("hi"), py::arg("out") = nullptr);
+  m.def(
+      "astype",
+      [](const Array& a, const py::object& d, const Array* out) {
+        const Dtype t = dtype_arg(d);
+        return traced("astype", {&a}, [&] { return astype_op(a, t, out); });
+      },
+      py::arg("a"), py::arg("dtype"), py::arg("out") = nullptr);
 
 #define RED(NAME, K)                                                                                      \
   m.def(                                                                                                  \
       #NAME,                                                                                              \
-      [](const Array& a, py::object axis, bool keepdims, const Array* out) { return reduce_py(a, axis, keepdims, out, K); }, \
+      [](const Array& a, py::object axis, bool keepdims, const Array* out) {                              \
+        return traced(#NAME, {&a}, [&] { return reduce_py(a, axis, keepdims, out, K); });                 \
+      },                                                                                                  \
       py::arg("a"), py::arg("axis") = py::none(), py::arg("keepdims") = false, py::arg("out") = nullptr);
   RED(sum, ReduceKernel::Sum)
   RED(prod, ReduceKernel::Prod)
@@ -433,7 +489,7 @@ PYBIND11_MODULE(_core, m) {
       [](const Array& a, py::object axis, const Array* out) {
         std::optional<ssize_t> ax;
         if (!axis.is_none()) ax = axis.cast<ssize_t>();
-        return cumsum_op(a, resolve_axis(ax, a.ndim()), out);
+        return traced("cumsum", {&a}, [&] { return cumsum_op(a, resolve_axis(ax, a.ndim()), out); });
       },
       py::arg("a"), py::arg("axis") = py::none(), py::arg("out") = nullptr);
 
@@ -450,7 +506,8 @@ PYBIND11_MODULE(_core, m) {
         py::arg("axis"));
   m.def("slice", &slice, py::arg("a"), py::arg("start"), py::arg("stop"), py::arg("step"));
   m.def("index_select", &index_select, py::arg("a"), py::arg("axis"), py::arg("index"));
-  m.def("contiguous", &contiguous, py::arg("a"));
+  m.def("contiguous", [](const Array& a) { return traced("contiguous", {&a}, [&] { return contiguous(a); }); },
+        py::arg("a"));
 
   // host <-> device
   m.def("_from_numpy", &from_numpy, py::arg("arr"), py::arg("dtype"), py::arg("device") = py::none());
@@ -471,10 +528,22 @@ PYBIND11_MODULE(_core, m) {
   m.def("synchronize", [](py::object d) {
     int dv = parse_device(d);
     py::gil_scoped_release nogil;
-    default_stream(dv)->synchronize();
-    check_rt(mpy_rt_set_device(dv), "set device");
-    check_rt(mpy_rt_device_synchronize(), "device synchronize");  // user streams too
+    synchronize_device(dv);  // every stream of the device, faults of each reported to that stream
   }, py::arg("device") = py::none());
+
+  // debug mode (rust/musapy-python/src/lib.rs:243-258, rust/musapy-core/src/debug.rs)
+  m.def("set_debug", [](bool enabled) { set_debug(enabled); }, py::arg("enabled"));
+  m.def("_is_debug", []() { return is_debug(); });
+  struct DebugContext {
+    bool prev = false;
+  };
+  py::class_<DebugContext>(m, "_DebugContext")
+      .def("__enter__", [](DebugContext& c) {
+        c.prev = is_debug();
+        set_debug(true);
+      })
+      .def("__exit__", [](DebugContext& c, py::object, py::object, py::object) { set_debug(c.prev); });
+  m.def("debug", []() { return DebugContext{}; });
   m.def("device_count", []() {
     int n = 0;
     if (mpy_rt_device_count(&n) != 0) return 0;

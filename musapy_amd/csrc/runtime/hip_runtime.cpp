@@ -66,7 +66,7 @@ struct Calls {
   hipError_t (*event_elapsed)(float*, hipEvent_t, hipEvent_t);
   hipError_t (*last_error)();  // the pending launch error, consumed
   hipError_t (*fill_u32)(void*, uint32_t, size_t, hipStream_t);
-  int (*take_fault)(int);      // the kernel library's device wait-fault word
+  int (*take_fault_ws)(void*, size_t, hipStream_t);  // a workspace's wait-fault word (kernel library)
 };
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
@@ -116,7 +116,7 @@ const Calls kHipCalls = {
       k_fill_u32<<<dim3(unsigned(g)), 256, 0, st>>>(static_cast<uint32_t*>(p), v, n);
       return hipGetLastError();
     },
-    [](int d) { return musapy_kernels_take_fault(d); },
+    [](void* ws, size_t n, hipStream_t st) { return musapy_kernels_take_fault_ws(ws, n, st); },
 };
 
 // The host-memory table: one fake device, memory from the C heap, streams and events as tokens,
@@ -161,7 +161,7 @@ const Calls kHostCalls = {
       for (size_t i = 0; i < nbytes / 4; ++i) q[i] = v;
       return hipSuccess;
     },
-    [](int) { return 0; },
+    [](void*, size_t, hipStream_t) { return 0; },
 };
 
 std::atomic<const Calls*> g_calls{&kHipCalls};
@@ -443,10 +443,10 @@ int mpy_rt_check_launch(void) {
   return w ? -w : 0;
 }
 
-int mpy_rt_take_fault(int device) {
+int mpy_rt_take_fault_ws(void* workspace, size_t workspace_bytes, hipStream_t stream) {
   int code = 0;
   if (injected(MPY_RT_CALL_FAULT, &code)) return code;
-  return H().take_fault(device);
+  return H().take_fault_ws(workspace, workspace_bytes, stream);
 }
 
 const char* mpy_rt_error_string(int code) {

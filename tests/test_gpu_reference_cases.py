@@ -465,3 +465,41 @@ class TestStreams:
             c = ms.add(b, b)
         s.synchronize()
         assert c.tolist() == [4.0, 8.0]
+
+    def test_stream_synchronize_pending_count(self):
+        """test_acceptance_v03.py:112-116: an explicit synchronize leaves nothing pending."""
+        s = ms.Stream("musa:0")
+        s.synchronize()
+        assert s.pending_count == 0
+
+
+# ---- test_debug_summary.py (TestDebugMode) ----------------------------------------------------
+class TestDebugMode:
+    """test_debug_summary.py:95-156, on the GPU device instead of the reference's CPU device."""
+
+    def test_set_debug_true_and_false(self):
+        ms.set_debug(True)
+        try:
+            s = ms.Stream()
+            with ms.stream(s):
+                c = ms.add(ms.array([1.0, 2.0], dtype="f32"), ms.array([3.0, 4.0], dtype="f32"))
+            assert s.pending_count == 1  # the add's OpContext (debug mode only)
+            assert c.tolist() == [4.0, 6.0]
+            assert s.pending_count == 0  # the readback's synchronize cleared it
+        finally:
+            ms.set_debug(False)
+        c = ms.add(ms.array([1.0], dtype="f32"), ms.array([2.0], dtype="f32"))
+        assert c.tolist() == [3.0]
+
+    def test_debug_context_manager_nested(self):
+        ms.set_debug(False)
+        with ms.debug():
+            with ms.debug():
+                c = ms.array([1.0], dtype="f32") + ms.array([2.0], dtype="f32")
+                assert c.tolist() == [3.0]
+            c = ms.array([1.0], dtype="f32") + ms.array([2.0], dtype="f32")
+            assert c.tolist() == [3.0]
+            assert ms._core._is_debug()
+        assert not ms._core._is_debug()
+        a, b = ms.array([1.0, 2.0, 3.0], dtype="f32"), ms.array([4.0, 5.0, 6.0], dtype="f32")
+        assert (a + b).tolist() == [5.0, 7.0, 9.0]

@@ -133,41 +133,141 @@ def test_chained_row_scan_gives_up_and_recovers():
     _fresh_stream_case(lambda: (ms.from_numpy(y),), lambda Y: ms.cumsum(Y, axis=1), check)
 
 
-def test_c_abi_fault_word_and_workspace_reuse():
-    """A caller of musapy_reduce_fused_v1 reads the fault with musapy_kernels_take_fault after its
-    synchronize, zeroes its workspace, and the next call is correct."""
+def _fused_lib():
     lib = _lib()
     P, I, SZ, SS = ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_ssize_t)
     lib.musapy_reduce_fused_v1.restype = ctypes.c_int
     lib.musapy_reduce_fused_v1.argtypes = [I, I, P, P, I, SZ, SS, I, ctypes.c_size_t, ctypes.c_size_t,
                                            ctypes.c_size_t, P, ctypes.c_size_t, P]
+    lib.musapy_kernels_take_fault_ws.restype = ctypes.c_int
+    lib.musapy_kernels_take_fault_ws.argtypes = [P, ctypes.c_size_t, P]
+    return lib
+
+
+def test_c_abi_fault_word_and_workspace_reuse():
+    """A caller of musapy_reduce_fused_v1 reads the fault in its own workspace's last word with
+    musapy_kernels_take_fault_ws after its synchronize; taking it zeroes the workspace, so the
+    next call on the same workspace is correct."""
+    lib = _fused_lib()
     RED_SUM, DT_F64 = 0, 11
     x = RNG.standard_normal((4, 1 << 18))
     X = ms.from_numpy(x)
     C = ms.from_numpy(np.zeros(4))
-    ws_words = 4 * 64 * 2
+    ws_words = 4 * 64 * 2 + 1  # the slots, then the fault word
     WS = ms.from_numpy(np.zeros(ws_words, np.uint64))
     shape = (ctypes.c_size_t * 2)(4, 1 << 18)
     strides = (ctypes.c_ssize_t * 2)(1 << 18, 1)
     ms.synchronize()
-    assert lib.musapy_kernels_take_fault(0) == 0
+    st = X.stream_ptr
+    assert lib.musapy_kernels_take_fault_ws(WS.data_ptr, ws_words * 8, st) == 0
 
     def call():
         return lib.musapy_reduce_fused_v1(RED_SUM, DT_F64, X.data_ptr, C.data_ptr, 2, shape, strides, 1, 1 << 18, 4,
-                                          64, WS.data_ptr, ws_words * 8, X.stream_ptr)
+                                          64, WS.data_ptr, ws_words * 8, st)
 
+    # one word short of the slots and the fault word: refused, nothing launched
+    assert lib.musapy_reduce_fused_v1(RED_SUM, DT_F64, X.data_ptr, C.data_ptr, 2, shape, strides, 1, 1 << 18, 4, 64,
+                                      WS.data_ptr, (ws_words - 1) * 8, st) == -1
     with _NoPolls(lib):
         assert call() == 0
         ms.synchronize()
-    assert lib.musapy_kernels_take_fault(0) == 1
-    assert lib.musapy_kernels_take_fault(0) == 0  # taking it clears it
-    WS2 = ms.from_numpy(np.zeros(ws_words, np.uint64))  # a late publisher may have left tags in WS
+    assert lib.musapy_kernels_take_fault(0) == 0  # the no-alloc scratch's word is not this one
+    assert lib.musapy_kernels_take_fault_ws(WS.data_ptr, ws_words * 8, st) == 1
+    assert not WS.numpy().any(), "taking the fault zeroes the workspace"
+    assert lib.musapy_kernels_take_fault_ws(WS.data_ptr, ws_words * 8, st) == 0
+    assert call() == 0
     ms.synchronize()
-    assert lib.musapy_reduce_fused_v1(RED_SUM, DT_F64, X.data_ptr, C.data_ptr, 2, shape, strides, 1, 1 << 18, 4, 64,
-                                      WS2.data_ptr, ws_words * 8, X.stream_ptr) == 0
-    ms.synchronize()
-    assert lib.musapy_kernels_take_fault(0) == 0
+    assert lib.musapy_kernels_take_fault_ws(WS.data_ptr, ws_words * 8, st) == 0
     got = C.numpy()
     want = R.reduce(x, "sum", 1)
     assert np.all(np.abs(got - want) <= 1e-12 * np.abs(x).sum(axis=1))
-    assert not WS2.numpy().any(), "the workspace is left zero"
+    assert not WS.numpy().any(), "the workspace is left zero"
+
+
+def test_fault_is_reported_to_the_stream_whose_wait_expired():
+    """Stream A queues a reduction that gives up (no polls), stream B one with the default limit.
+    B's synchronize is clean and B is not poisoned; A's synchronize raises KernelError and poisons
+    A; the next reduction on A is exact again (rust/musapy-core/src/stream.rs:311-377 poisons the
+    stream whose synchronize failed)."""
+    lib = _lib()
+    x = RNG.standard_normal(1 << 22).astype(np.float32)
+    y = RNG.standard_normal((8, 1 << 20)).astype(np.float32)
+    a_s, b_s = ms.Stream(), ms.Stream()
+    with ms.stream(a_s):
+        X = ms.from_numpy(x)
+    with ms.stream(b_s):
+        Y = ms.from_numpy(y)
+    ms.synchronize()
+    with ms.stream(a_s):
+        with _NoPolls(lib):
+            bad = ms.argmax(X)
+    with ms.stream(b_s):
+        good = ms.argmax(Y, axis=1)
+    b_s.synchronize()
+    assert not b_s.is_poisoned
+    assert_bits_equal(good.numpy(), R.reduce(y, "argmax", 1), "stream B's reduction")
+    with pytest.raises(ms.KernelError, match="device wait expired"):
+        a_s.synchronize()
+    assert a_s.is_poisoned and not b_s.is_poisoned
+    del bad
+    with ms.stream(a_s):
+        again = ms.argmax(X).numpy()
+    assert_bits_equal(again, R.reduce(x, "argmax", None), "stream A after the fault")
+    assert not b_s.is_poisoned
+
+
+def test_device_synchronize_poisons_only_the_faulting_stream():
+    """ms.synchronize() checks every stream with bounded waits queued: the one whose scan gave up
+    raises and is poisoned, the other stream's results are exact and it stays clean."""
+    lib = _lib()
+    y = RNG.random((520, 20_000))
+    x = RNG.standard_normal((4096, 2048)).astype(np.float32)
+    a_s, b_s = ms.Stream(), ms.Stream()
+    with ms.stream(a_s):
+        Y = ms.from_numpy(y)
+    with ms.stream(b_s):
+        X = ms.from_numpy(x)
+    ms.synchronize()
+    with ms.stream(a_s):
+        with _NoPolls(lib):
+            ms.cumsum(Y, axis=1)
+    with ms.stream(b_s):
+        s0 = ms.sum(X, axis=0)
+    with pytest.raises(ms.KernelError, match="device wait expired in a cumsum"):
+        ms.synchronize()
+    assert a_s.is_poisoned and not b_s.is_poisoned
+    want = R.reduce(x, "sum", 0)
+    assert np.all(np.abs(s0.numpy() - want) <= 1e-5 * np.abs(x).sum(axis=0))
+    ms.synchronize()  # nothing left to report
+
+
+def test_reference_signature_scan_reports_in_its_scratch():
+    """musapy_cumsum_f64_v3 (the reference's signature) keeps its fault word in the last 8 bytes
+    of the scratch capacity the reference's formula gives (op_builder.rs:3315-3321)."""
+    lib = _lib()
+    P, I, SZ, SS, U = (ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t),
+                       ctypes.POINTER(ctypes.c_ssize_t), ctypes.c_size_t)
+    lib.musapy_cumsum_f64_v3.restype = None
+    lib.musapy_cumsum_f64_v3.argtypes = [P, P, P, I, SZ, SS, I, U, U, P]
+    lib.musapy_kernels_take_fault_ws.restype = ctypes.c_int
+    lib.musapy_kernels_take_fault_ws.argtypes = [P, U, P]
+    rows, L = 4, 100_000
+    y = RNG.random((rows, L))
+    bpr = (L + 255) // 256
+    cap = rows * (bpr + (bpr + 255) // 256 if bpr > 256 else bpr)
+    Y = ms.from_numpy(y)
+    O = ms.from_numpy(np.zeros_like(y))
+    T = ms.from_numpy(np.full(cap, 7.0))  # garbage: the launch clears what it uses
+    shape = (ctypes.c_size_t * 2)(rows, L)
+    strides = (ctypes.c_ssize_t * 2)(L, 1)
+    ms.synchronize()
+    st = Y.stream_ptr
+    with _NoPolls(lib):
+        lib.musapy_cumsum_f64_v3(Y.data_ptr, O.data_ptr, T.data_ptr, 2, shape, strides, 1, L, rows * L, st)
+        ms.synchronize()
+    assert lib.musapy_kernels_take_fault_ws(T.data_ptr, cap * 8, st) == 2
+    lib.musapy_cumsum_f64_v3(Y.data_ptr, O.data_ptr, T.data_ptr, 2, shape, strides, 1, L, rows * L, st)
+    ms.synchronize()
+    assert lib.musapy_kernels_take_fault_ws(T.data_ptr, cap * 8, st) == 0
+    want = R.cumsum(y, 1)
+    assert np.all(np.abs(O.numpy() - want) <= 1e-12 * np.abs(want))

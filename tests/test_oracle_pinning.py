@@ -63,6 +63,42 @@ def test_pow_special_cases():
     assert np.array_equal(np.isnan(got), np.isnan(want)) and np.all((got == want) | np.isnan(want))
 
 
+def _pow_samples(n):
+    """Positive bases over six decades with exponents that keep the result finite, plus negative
+    bases with integral exponents (odd and even: the sign of the result depends on the parity)."""
+    base = np.exp(RNG.uniform(np.log(1e-3), np.log(1e3), n))
+    expo = RNG.uniform(-12, 12, n)
+    nb = n // 4
+    base[:nb] = -RNG.uniform(0.05, 20.0, nb)
+    expo[:nb] = RNG.integers(-9, 10, nb).astype(np.float64)
+    return base, expo
+
+
+def test_pow_f32_close_to_exact():
+    """f32 pow against the f64 evaluation rounded once to f32 (f64 pow is within 1 ulp of f64,
+    far below half an ulp of f32)."""
+    a, b = _pow_samples(20000)
+    a32, b32 = a.astype(np.float32), b.astype(np.float32)
+    got = R.binary("pow", a32, b32)
+    want = np.power(a32.astype(np.float64), b32.astype(np.float64)).astype(np.float32)
+    ok = np.isfinite(want) & (want != 0)
+    assert ok.sum() > 19000
+    assert ulp_diff_f32(got[ok], want[ok]).max() <= 1
+    # negative base, integral exponent: the sign follows the exponent's parity
+    neg = (a32 < 0) & ok
+    assert np.array_equal(np.signbit(got[neg]), np.signbit(want[neg]))
+
+
+def test_pow_f64_close_to_exact():
+    """f64 pow against x87 extended precision (64-bit mantissa), rounded once to double."""
+    a, b = _pow_samples(20000)
+    got = R.binary("pow", a, b)
+    want = np.power(a.astype(np.longdouble), b.astype(np.longdouble)).astype(np.float64)
+    ok = np.isfinite(want) & (want != 0)
+    assert ok.sum() > 19000
+    assert ulp_diff_f64(got[ok], want[ok]).max() <= 1
+
+
 # ---- unary ----
 def _exact_f32(fn, x):
     """float32 result of `fn` evaluated in float64 (error <= 1 ulp(f64) << 0.5 ulp(f32))."""

@@ -161,6 +161,55 @@ def event(name):
     results[name + "_live_delta"] = live() - before
 
 
+@case
+def debug_ctx(name):
+    """Debug mode records an OpContext per op (op_builder.rs:507-521); a failing synchronize names
+    the oldest pending op (stream.rs:367-373) and a clean one clears them."""
+    ms.set_debug(False)
+    s = ms.Stream()
+    with ms.stream(s):
+        a = ms.from_numpy(A)
+        ms.add(a, a)
+        results[name + "_off_pending"] = s.pending_count
+        ms.set_debug(True)
+        b = ms.mul(a, a)
+        ms.sum(b, 0)
+        results[name + "_on_pending"] = s.pending_count
+        lib.mpy_rt_inject(SYNC, 700, 0, 1)
+        expect(name, ms.StreamError, lambda: s.synchronize())
+        results[name + "_after_fail"] = s.pending_count      # a failed synchronize keeps them
+        expect(name, None, lambda: s.synchronize())
+        results[name + "_after_clean"] = s.pending_count
+        ms.cumsum(a, 1)
+        lib.mpy_rt_inject(FAULT, 1, 0, 1)
+        expect(name, ms.KernelError, lambda: s.synchronize())
+        ms.set_debug(False)
+        with ms.debug():
+            results[name + "_ctx_on"] = ms._core._is_debug()
+            with ms.debug():
+                pass
+            results[name + "_ctx_nested"] = ms._core._is_debug()
+        results[name + "_ctx_off"] = ms._core._is_debug()
+        results[name + "_stream_id"] = s.id
+
+
+@case
+def device_sync(name):
+    """ms.synchronize() reads the fault word of every stream with bounded waits queued and poisons
+    only the stream that reports one."""
+    s1, s2 = ms.Stream(), ms.Stream()
+    with ms.stream(s1):
+        a = ms.from_numpy(A)
+        ms.cumsum(a, 1)                                 # bounded waits on s1
+    with ms.stream(s2):
+        b = ms.from_numpy(A)
+        ms.add(b, b)                                    # none on s2
+    lib.mpy_rt_inject(FAULT, 1, 0, 1)
+    expect(name, ms.KernelError, lambda: ms.synchronize())
+    results[name + "_poisoned"] = [bool(s1.is_poisoned), bool(s2.is_poisoned)]
+    expect(name, None, lambda: ms.synchronize())
+
+
 if "--sweep" in sys.argv:
     rng = np.random.default_rng(5)
     shapes = [(), (1,), (7,), (3, 5), (4, 1, 6), (2, 3, 4, 5), (0, 3), (5, 0)]
@@ -238,6 +287,25 @@ def test_wait_fault_read_only_after_bounded_waits(plain):
     assert _kinds(plain, "fault") == ["none", "KernelError", "none"]
     assert plain["fault_clean"] is True and plain["fault_poisoned"] is True
     assert "device wait expired" in plain["fault"][1][1]
+
+
+def test_debug_mode_attributes_stream_failures_to_the_oldest_op(plain):
+    assert _kinds(plain, "debug_ctx") == ["StreamError", "none", "KernelError"]
+    assert plain["debug_ctx_off_pending"] == 0
+    assert plain["debug_ctx_on_pending"] == 2
+    assert plain["debug_ctx_after_fail"] == 2 and plain["debug_ctx_after_clean"] == 0
+    sid = plain["debug_ctx_stream_id"]
+    msg = plain["debug_ctx"][0][1]
+    assert f"| failed op: op 'mul' on stream {sid}, inputs=[(4, 6) f32, (4, 6) f32] at <string>:" in msg, msg
+    assert "(debug_ctx)" in msg, msg
+    assert f"failed op: op 'cumsum' on stream {sid}, inputs=[(4, 6) f32]" in plain["debug_ctx"][2][1]
+    assert plain["debug_ctx_ctx_on"] is True and plain["debug_ctx_ctx_nested"] is True
+    assert plain["debug_ctx_ctx_off"] is False
+
+
+def test_device_synchronize_reports_the_faulting_stream(plain):
+    assert _kinds(plain, "device_sync") == ["KernelError", "none"]
+    assert plain["device_sync_poisoned"] == [True, False]
 
 
 def test_allocation_failure_retries_then_raises(plain):

@@ -23,7 +23,7 @@ P, I, U = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 SZ, SS = ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_ssize_t)
 OPS = {"sum": 0, "prod": 1, "max": 2, "min": 3, "mean": 4, "argmax": 5, "argmin": 6}
 DT = {np.int64: 4, np.float32: 10, np.float64: 11, np.complex64: 13, np.complex128: 14}
-SCRATCH_BYTES = 1 << 20
+SCRATCH_BYTES = (1 << 20) + 256  # as the library's scratch: 1 MiB of slots, then a line ending in its fault word
 
 
 def lib():
@@ -35,6 +35,8 @@ def lib():
     L.musapy_kernels_take_error.restype = ctypes.c_int
     L.musapy_kernels_take_fault.restype = ctypes.c_int
     L.musapy_kernels_take_fault.argtypes = [ctypes.c_int]
+    L.musapy_kernels_set_spin_limit.restype = ctypes.c_uint32
+    L.musapy_kernels_set_spin_limit.argtypes = [ctypes.c_uint32]
     return L
 
 
@@ -172,3 +174,31 @@ def test_noalloc_refuses_more_slots_than_the_scratch_holds():
     assert r == 0
     ms.synchronize()
     assert_bits_equal(C.numpy(), R.reduce(x, "max", 1), "noalloc max after the refused call")
+
+
+def test_noalloc_fault_is_taken_once_and_the_next_call_starts_clean():
+    """A no-alloc reduction whose combiner gives up (no polls allowed) reports through the
+    scratch's fault word, once; the next no-alloc call zeroes the scratch on its own stream first
+    and matches the workspace entry point bit for bit, twice in a row (the second smaller)."""
+    L = lib()
+    x = data("sum", np.float32, (1 << 21) + 333)
+    X = ms.from_numpy(x)
+    C = ms.from_numpy(np.zeros(1, np.float32))
+    shape = (ctypes.c_size_t * 1)(x.size)
+    strides = (ctypes.c_ssize_t * 1)(1)
+    ms.synchronize()
+    assert L.musapy_kernels_take_fault(0) == 0
+    prev = L.musapy_kernels_set_spin_limit(0)
+    try:
+        r = L.musapy_reduce_fused_noalloc_v1(OPS["sum"], DT[np.float32], X.data_ptr, C.data_ptr, 1, shape, strides, 0,
+                                             x.size, 1, 512, X.stream_ptr)
+    finally:
+        L.musapy_kernels_set_spin_limit(prev)
+    assert r == 0
+    ms.synchronize()
+    assert L.musapy_kernels_take_fault(0) == 1
+    assert L.musapy_kernels_take_fault(0) == 0  # reported once
+    for n, tiles in ((1 << 21) + 333, 512), ((1 << 19) + 5, 64):
+        got, ref = reduce_both(L, "sum", np.float32, x[:n], tiles)
+        assert_bits_equal(got, ref, f"noalloc after a fault, n={n}", nan_bits=True)
+        check_oracle("sum", got, x[:n])
