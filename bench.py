@@ -37,6 +37,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--all", action="store_true", help="also time every BASELINE config (table on stderr)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--keys", metavar="K1,K2", help="with --all: time only these config keys")
     p.add_argument("--only", metavar="KEY",
                    help="launch one op warmup+steps times and exit (a step op: add, sum, argmax; the "
                         "calibration copy: copy; or a config key of --all, e.g. cumsum, max01): the "
@@ -283,6 +284,20 @@ def all_config_ops(ms, host_legs=False):
         xt = [ms.transpose(c) for c in up(h, k)]
         return row(lambda i: ms.exp(xt[i % k]), 8 * 33_554_432, leg(lambda: R.unary("exp", h.T), 8 * 33_554_432), k)
 
+    def b_xTc2():
+        # the copy of C2's transposed view (what exp adds to it: b_expT against this row)
+        h = get("xe", lambda: np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32))
+        k = ncopies(h)
+        xt = [ms.transpose(c) for c in up(h, k)]
+        return row(lambda i: ms.contiguous(xt[i % k]), 8 * 33_554_432, k=k)
+
+    def b_exp32():
+        # exp of a contiguous array of C2's size (the transcendental's cost without the transpose)
+        h = get("xe", lambda: np.random.default_rng(0).uniform(-4, 4, (8192, 4096)).astype(np.float32))
+        k = ncopies(h)
+        X = up(h, k)
+        return row(lambda i: ms.exp(X[i % k]), 8 * 33_554_432, k=k)
+
     def b_c3add():
         i64h, f64h, _, _, _ = c3()
         k = ncopies(i64h, f64h)
@@ -422,6 +437,8 @@ def all_config_ops(ms, host_legs=False):
         ("argmax256", "full argmax f32 256M", b_argmax256),
         ("bcast", "C2 broadcast add (4096,1)+(8192,)", b_bcast),
         ("expT", "C2 exp transposed (8192,4096)^T", b_expT),
+        ("xTc2", "contiguous of C2's transposed view f32 (8192,4096)^T", b_xTc2),
+        ("exp32", "exp f32 contiguous (8192,4096)", b_exp32),
         ("c3add", "C3 add i64+f64->f64 (fused promotion)", b_c3add),
         ("clamp", "C3 clamp f64", b_clamp),
         ("f64f32", "C3 astype f64->f32", b_f64f32),
@@ -636,7 +653,10 @@ def main():
     if args.all:
         del ops, host
         rows = []
+        wanted = set(args.keys.split(",")) if args.keys else None
         for key, name, build in all_config_ops(ms, host_legs=not args.no_cpu):
+            if wanted is not None and key not in wanted:
+                continue
             gc.collect()  # free the previous row's device arrays before this row is timed
             fn, bytes_, cpu = build()
             row = {"op": name, "key": key}

@@ -138,6 +138,34 @@ struct CastF {
   __device__ D operator()(S v) const { return static_cast<D>(v); }
 };
 
+// 64-bit integer -> f32, rounded to nearest even, from 32-bit operations only.  The compiler's own
+// lowering shifts the value with v_lshlrev_b64 by a count that the instruction just before it
+// computes; in instances measured on gfx950 (transpose tiles of 256 rows x 16 lanes and of 64 rows
+// x 64 lanes) that shift used a stale count in whole waves, for the second conversion of each
+// pair, returning values such as -1.0 for -721.  Here the leading word is formed with a funnel
+// shift (v_alignbit_b32) and a sticky bit for the bits below it, and rounded once by
+// v_cvt_f32_u32: a 32-bit word whose top bit is set rounds to 24 bits at bit 8, and the sticky
+// bit in bit 0 keeps ties and near-ties apart, so the result is the correctly rounded value.
+__device__ inline float u64_to_f32(uint64_t m) {
+  const uint32_t hi = uint32_t(m >> 32), lo = uint32_t(m);
+  if (hi == 0) return __uint2float_rn(lo);
+  const uint32_t lz = __clz(hi);  // 0..31: (hi:lo) << lz has its top bit set
+  const uint32_t top = lz == 0 ? hi : __builtin_amdgcn_alignbit(hi, lo, 32u - lz);
+  const uint32_t below = lo << lz;  // the bits shifted out of the leading word (a 32-bit shift)
+  return ldexpf(__uint2float_rn(top | (below != 0 ? 1u : 0u)), int(32 - lz));
+}
+__device__ inline float i64_to_f32(int64_t x) {
+  const uint64_t m = x < 0 ? uint64_t(0) - uint64_t(x) : uint64_t(x);  // |INT64_MIN| = 2^63 fits
+  const float r = u64_to_f32(m);
+  return x < 0 ? -r : r;
+}
+template <> struct CastF<int64_t, float> {
+  __device__ float operator()(int64_t v) const { return i64_to_f32(v); }
+};
+template <> struct CastF<uint64_t, float> {
+  __device__ float operator()(uint64_t v) const { return u64_to_f32(v); }
+};
+
 // float -> i64 saturates at the range ends and maps NaN to 0 (Rust `as`, since 1.45).
 template <class S>
 __device__ inline int64_t sat_to_i64(S v) {
