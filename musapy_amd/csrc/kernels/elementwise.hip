@@ -291,6 +291,7 @@ struct TransposeArgs {
   RowIndexer<2> batch;     // batch dims: [0] output strides, [1] input strides
   bool vec_in, vec_out;    // 16-byte aligned vector access possible on each side
   bool nt;                 // streaming loads
+  bool pmajor;             // consecutive blocks take consecutive tiles along P (else along L)
 };
 
 // Tile geometry: PL lanes x VI elements along P (input-contiguous) by TL along L
@@ -310,9 +311,14 @@ template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
 //    permute: 91.0-92.1 us, against 95.1 us over 256 rows).
 // The rows are halved until the tile's LDS fits in 68 KB (wide outputs of narrow inputs).
 // Block order: consecutive blocks take consecutive tiles along L (the output rows), so the blocks
-// in flight write whole output rows.  Groups of 1-16 L tiles taken along P first measured slower
+// in flight write whole output rows, except when the output rows are longer than the input rows
+// (then along P, launch_transpose).  Groups of 1-16 L tiles taken along P first measured slower
 // for the (8192, 8192) f32 X^T (93.5-97.8 us against 90.0-90.3), level for c128 and exp, and only
-// the (8192, 128, 64) permute gained (89.8-91.0 against 92.4-92.5 us).
+// the (8192, 128, 64) permute gained (89.8-91.0 against 92.4-92.5 us).  Also measured for C2's
+// (8192, 4096) view and not kept: the functor applied on the store side (LDS holding the input),
+// exp 52.6 against 51.6 us; software-pipelined blocks of 2-4 tiles (next tile's loads in flight,
+// LDS-only barriers), 52.3-56 us; the block -> tile map grouped by XCD, level; 16 lanes x 256 rows
+// (50.3 us, but X^T 97.3 us) and 8 x 512, 16 x 256 in 512 lanes, 32 x 128 in 512 lanes (53-55 us).
 template <class F> struct tr_moves_only : std::false_type {};  // copies and casts
 template <> struct tr_moves_only<IdentityF> : std::true_type {};
 template <class S, class D> struct tr_moves_only<CastF<S, D>> : std::true_type {};
@@ -338,10 +344,18 @@ __global__ __launch_bounds__(BS) void k_unary_transpose(const TI* __restrict__ a
   static_assert(BS % LPW == 0 && TP % (BS / LPW) == 0, "write passes must tile TP");
   __shared__ TO tile[TL][TP + 1];
   const uint32_t id = blockIdx.x;
-  const uint32_t bq = fd_div(ta.tilesL, id);
-  const uint32_t tl = id - bq * ta.tilesL.d;
-  const uint32_t batch = fd_div(ta.tilesP, bq);
-  const uint32_t tp = bq - batch * ta.tilesP.d;
+  uint32_t tl, tp, batch;
+  if (ta.pmajor) {
+    const uint32_t bq = fd_div(ta.tilesP, id);
+    tp = id - bq * ta.tilesP.d;
+    batch = fd_div(ta.tilesL, bq);
+    tl = bq - batch * ta.tilesL.d;
+  } else {
+    const uint32_t bq = fd_div(ta.tilesL, id);
+    tl = id - bq * ta.tilesL.d;
+    batch = fd_div(ta.tilesP, bq);
+    tp = bq - batch * ta.tilesP.d;
+  }
   int64_t off[2];
   row_offsets<2>(ta.batch, batch, off);
   const uint64_t p0 = uint64_t(tp) * TP, l0 = uint64_t(tl) * TL;
@@ -420,12 +434,21 @@ bool launch_transpose_tiles(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, b
 }
 
 template <class F, class TO, class TI>
-bool launch_transpose(const TI* a, TO* c, const TransposeArgs& ta, uint64_t nb, bool nts, hipStream_t st, F f) {
+bool launch_transpose(const TI* a, TO* c, TransposeArgs ta, uint64_t nb, bool nts, hipStream_t st, F f) {
   // LDS per tile: TL x (PL*VI + 1) elements of TO (tr_tl); 32 lanes x 128 rows is 66 KB for f32
   if (ta.P * 4 <= uint64_t(tr_tp<TI, 32>()))
     return launch_transpose_tiles<F, TO, TI, 8, 1024, 256>(a, c, ta, nb, nts, st, f);
   if (ta.P * 2 <= uint64_t(tr_tp<TI, 32>()))
     return launch_transpose_tiles<F, TO, TI, 16, 1024, 128>(a, c, ta, nb, nts, st, f);
+  // Output rows longer than the input rows: tiles taken along P first, so that the blocks in flight
+  // read whole input rows, each functor in the copy's 1024-lane tile.  (8192, 4096) f32 transposed
+  // (C2's view, L = 8192 > P = 4096), event-timed: copy 50.5-51.9 -> 48.5-49.4 us, exp
+  // 51.5-51.9 -> 49.6-49.9 us.  Square shapes keep the L order (X^T f32 at (8192, 8192): 91.7-92.2
+  // us against 96.1-96.7 us taken along P).
+  if (ta.L > ta.P) {
+    ta.pmajor = true;
+    return launch_transpose_tiles<F, TO, TI, 32, 1024, 128>(a, c, ta, nb, nts, st, f);
+  }
   if constexpr (tr_moves_only<F>::value)
     return launch_transpose_tiles<F, TO, TI, 32, 1024, 128>(a, c, ta, nb, nts, st, f);
   else
