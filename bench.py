@@ -362,6 +362,17 @@ def all_config_ops(ms, host_legs=False):
         yh = get("y", lambda: np.random.default_rng(0).random((1024, 65536)))
         return row(None, 16 * 65536, leg(lambda: R.cumsum(yh[:1], axis=1, literal=True), 16 * 65536))
 
+    def b_copy64():
+        # C5's bytes (512 MB in, 512 MB out) as a plain copy: the rate a read-once, write-once f64
+        # stream reaches, beside the chained scan (a unit-stride view 1024 elements in, so that
+        # contiguous() copies)
+        m = 1024 * 65536
+        h = get("y", lambda: np.random.default_rng(0).random((1024, 65536))).reshape(-1)
+        h = np.concatenate([np.zeros(1024), h])
+        k = ncopies(h)
+        Y = up(h, k)
+        return row(lambda i: ms.contiguous(ms.slice(Y[i % k], [(1024, 1024 + m, 1)])), 16 * m, k=k)
+
     def b_csum():
         k = ncopies(zh())
         Z = up(zh(), k)
@@ -451,6 +462,7 @@ def all_config_ops(ms, host_legs=False):
         ("argmin1", "C4 argmin axis=1", b_c4("argmin", 1, 4 * n + 8 * 8192)),
         ("cumsum", "C5 cumsum f64 (1024,65536) axis=1", b_cumsum),
         ("cumsum_literal", "C5 cumsum f64, literal O(L^2) CPU form (1 of 1024 rows)", b_cumsum_literal),
+        ("copy64", "contiguous f64 67,108,864 (C5's bytes as a plain copy)", b_copy64),
         ("csum", "C5 c64 sum axis=(1,2)", b_csum),
         ("lt", "cmp lt f32 64M -> bool", b_lt),
         ("eqf64", "cmp eq f64 16M -> bool", b_eqf64),

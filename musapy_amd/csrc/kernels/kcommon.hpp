@@ -168,6 +168,16 @@ inline void with_store_policy(bool nt, L&& launch) {
   if (nt) launch(std::true_type{}); else launch(std::false_type{});
 }
 
+// Block-wide barrier that orders LDS accesses only.  __syncthreads() also waits until every
+// global load and store the wave has issued is complete (s_waitcnt vmcnt(0) before s_barrier),
+// so a barrier that follows a hand-over store would hold the whole block for that store's round
+// trip; where the barrier only publishes LDS values, this one lets such stores stay in flight.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------------------------
 // Wavefront-64 butterfly helpers (ds_swizzle/dpp are chosen by the compiler for __shfl_xor).
 template <typename T>

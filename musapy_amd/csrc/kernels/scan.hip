@@ -264,7 +264,7 @@ __global__ __launch_bounds__(kLbBlock) void k_scan_lookback(const T* __restrict_
     }
     if (lane == 0) s_prefix = P;
   }
-  __syncthreads();
+  lds_barrier();  // the prefix is in LDS; the publish stores stay in flight
   const A P = s_prefix;
 
   if (full) {
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* _
     if (lane == kWave - 1) s_wave[u][wv] = incl[u];
     incl[u] = wave_shr1(incl[u]);  // from here on: the lane's exclusive offset in its wave
   }
-  __syncthreads();
+  lds_barrier();  // thread 0's load of the predecessor's prefix stays in flight
   // exclusive offset of each lane's run inside the tile, and the tile aggregate (fixed order):
   // lanes 0 .. kWaves-1 read the sub-tile's wave totals and scan them, and every lane takes its
   // wave's exclusive offset and the sub-tile total from that scan (one LDS read per lane)
@@ -418,7 +418,9 @@ __global__ __launch_bounds__(BS) void k_scan_chain(const T* __restrict__ a, T* _
     if (chunk + 1 < sa.tiles) publish_value<W>(rowp + uint64_t(chunk) * W, bits_of(A(P + agg)));
     s_prefix = P;
   }
-  __syncthreads();
+  // LDS only: with __syncthreads() every lane's output stores waited for thread 0's publish and
+  // clear stores to complete, a store round trip per tile
+  lds_barrier();
   const A P = s_prefix;
 
   if (full) {
