@@ -25,6 +25,13 @@ namespace mpy {
 
 constexpr int kRBlock = 256;
 constexpr int kRowBS = 512;  // block size of the block-per-segment row kernel (measured best on MI355X)
+// Whole-array reductions: 256-lane blocks, each lane keeping 8 x 16-byte loads in flight (32 KB
+// chunks).  At a quarter of the waves of 512-lane blocks with 4 loads per lane, a 64M f32 sum with
+// its hand-over measured 40.5 us event-timed against 41.4-41.5 us (a one-round grid of 1024
+// blocks; 2048 blocks 40.9 us, 4096 blocks 41.5-42.1 us): the 8192 waves of the previous grid
+// took the dispatcher about 3.6 us to start.
+constexpr int kAllBS = 256;
+constexpr int kAllUnroll = 8;
 
 // what a kernel writes per (output, tile)
 enum : int { kWriteFinal = 0, kWriteVal = 1, kWritePair = 2 };
@@ -396,16 +403,16 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
 //
 // One streaming block's lane accumulator (before the block reduction); `first` receives element 0
 // on lane 0 of the block that reads it.
-template <class OpF, class T, int VEC, int UNROLL>
+template <class OpF, class T, int VEC, int UNROLL, int BS>
 __device__ inline typename OpF::A all_stream(const T* __restrict__ a, uint64_t n, uint32_t grid, uint64_t whole_q,
                                              uint32_t whole_r, uint32_t b, T& first) {
   using AF = typename OpF::A;
-  constexpr uint64_t kChunk = uint64_t(kRowBS) * UNROLL * VEC;
+  constexpr uint64_t kChunk = uint64_t(BS) * UNROLL * VEC;
   AF acc = OpF::init();
   // The lane's running accumulator (absolute int64 indices) continues from chunk to chunk, so
   // an ordered fold searches a chunk only when the chunk beats it.  Whole chunks are software
   // pipelined: the next chunk's loads are in flight while the current one is folded.
-  constexpr uint32_t stepk = uint32_t(kRowBS) * VEC;
+  constexpr uint32_t stepk = uint32_t(BS) * VEC;
   const uint64_t whole = n / kChunk;
   uint64_t c = b;
   Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers: no register copies between chunks
@@ -449,19 +456,15 @@ __device__ inline typename OpF::A all_stream(const T* __restrict__ a, uint64_t n
   }
   if (c == whole && whole * kChunk < n) {  // the last, partial chunk
     T f{};
-    acc = accumulate_segment<OpF, T, kRowBS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
-                                                          true, f, acc, int64_t(c * kChunk));
+    acc = accumulate_segment<OpF, T, BS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
+                                                      true, f, acc, int64_t(c * kChunk));
     if (c == 0) first = f;
   }
   return acc;
 }
 
-// f32 instances are held to 64 VGPRs (8 waves per SIMD, 4 blocks per CU): the 8-slot combiner
-// would otherwise take them to 68 and a quarter of the resident blocks
-template <class T>
-constexpr int all_fused_waves() { return sizeof(T) == 4 ? 8 : 1; }
 template <class Op, class OpF, class T, int VEC, int UNROLL, int PER>
-__global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fused(const T* __restrict__ a, uint64_t n, uint32_t grid,
+__global__ __launch_bounds__(kAllBS) void k_reduce_all_fused(const T* __restrict__ a, uint64_t n, uint32_t grid,
                                                              uint64_t whole_q, uint32_t whole_r, RedOut<T> out,
                                                              FusedArgs fa) {
   using AF = typename OpF::A;
@@ -470,8 +473,8 @@ __global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fus
   const uint32_t b = blockIdx.x;
   if (b < grid) {
     T first{};
-    AF acc = all_stream<OpF, T, VEC, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
-    acc = group_reduce<OpF, kRowBS>(acc, n < 0xffffffffull);
+    AF acc = all_stream<OpF, T, VEC, UNROLL, kAllBS>(a, n, grid, whole_q, whole_r, b, first);
+    acc = group_reduce<OpF, kAllBS>(acc, n < 0xffffffffull);
     if (threadIdx.x == 0) {
       if (b == 0 && n > 0) acc = absorb_first<OpF, T>(acc, first);
       uint32_t s[W];
@@ -480,14 +483,14 @@ __global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fus
     }
     return;
   }
-  // combiner: lane l folds block results l, l + 512, ... (PER of them at most)
+  // combiner: lane l folds block results l, l + kAllBS, ... (PER of them at most)
   uint64_t v[PER][W];
-  const bool ok = gather_published<W, PER>(fa.slots, grid, fa.spin_limit, v);
+  const bool ok = gather_published<W, PER, kAllBS>(fa.slots, grid, fa.spin_limit, v);
   AF r = OpF::init();
   AF first{};
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const uint32_t bb = threadIdx.x + j * kRowBS;
+    const uint32_t bb = threadIdx.x + j * kAllBS;
     if (bb >= grid) break;
     uint32_t s[W];
 #pragma unroll
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fus
     r = OpF::comb(r, x);
   }
   if (!combiner_gave_up(ok, fa.fault)) {  // uniform over the block
-    r = group_reduce<OpF, kRowBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
+    r = group_reduce<OpF, kAllBS>(r, n < 0xffffffffull);  // an absorbed NaN is put back below
     if (threadIdx.x == 0) {
       if constexpr (Op::kOrdered) {
         if (first.idx == 0 && is_nan(first.val)) r = first;  // block 0 absorbed a NaN at position 0
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(kRowBS, all_fused_waves<T>()) void k_reduce_all_fus
   // reaches memory), which cost 0.7 us per barrier in the combiner of a 64M argmax.
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const uint32_t bb = threadIdx.x + j * kRowBS;
+    const uint32_t bb = threadIdx.x + j * kAllBS;
     if (bb < grid) {
 #pragma unroll
       for (int i = 0; i < W; ++i) st_relaxed(fa.slots + uint64_t(bb) * W + i, 0);
@@ -535,25 +538,25 @@ __device__ inline void publish_key(uint64_t* slot, uint64_t key) { st_relaxed(sl
 // The largest of `count` published keys (lane l: slots l, l + kRowBS, ...), on thread 0, and
 // whether every slot was published within the poll budget (uniform over the block).  The slots go
 // back to zero after the block's last barrier, which would otherwise wait for those stores.
-template <int PER>
+template <int PER, int BS = kRowBS>
 __device__ inline bool fold_keys(uint64_t* slots, uint64_t count, uint32_t spin_limit, uint32_t* fault,
                                  uint64_t& key) {
   constexpr int kGroup = PER < 8 ? PER : 8;  // slots of a lane gathered at once
   key = 0;
   bool ok = true;
 #pragma clang loop unroll(disable)
-  for (uint64_t base = 0; base < count; base += uint64_t(kGroup) * kRowBS) {
+  for (uint64_t base = 0; base < count; base += uint64_t(kGroup) * BS) {
     uint64_t v[kGroup];
     uint32_t pending = 0;
 #pragma unroll
     for (int j = 0; j < kGroup; ++j) {
       v[j] = 0;
-      if (base + threadIdx.x + uint64_t(j) * kRowBS < count) pending |= 1u << j;
+      if (base + threadIdx.x + uint64_t(j) * BS < count) pending |= 1u << j;
     }
     for (uint32_t spins = 0; pending != 0 && spins < spin_limit; ++spins) {
 #pragma unroll
       for (int j = 0; j < kGroup; ++j)
-        if (pending & (1u << j)) v[j] = ld_relaxed(slots + base + threadIdx.x + uint64_t(j) * kRowBS);
+        if (pending & (1u << j)) v[j] = ld_relaxed(slots + base + threadIdx.x + uint64_t(j) * BS);
 #pragma unroll
       for (int j = 0; j < kGroup; ++j)
         if (v[j] != 0) pending &= ~(1u << j);
@@ -573,34 +576,34 @@ __device__ inline bool fold_keys(uint64_t* slots, uint64_t count, uint32_t spin_
       const uint64_t o = acc_shfl(key, m);
       key = o > key ? o : key;
     }
-    __shared__ uint64_t part[kRowBS / kWave];
+    __shared__ uint64_t part[BS / kWave];
     if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = key;
     __syncthreads();
     if (threadIdx.x == 0) {
 #pragma unroll
-      for (int i = 1; i < kRowBS / kWave; ++i) key = part[i] > key ? part[i] : key;
+      for (int i = 1; i < BS / kWave; ++i) key = part[i] > key ? part[i] : key;
     }
   }
-  for (uint64_t bb = threadIdx.x; bb < count; bb += kRowBS) st_relaxed(slots + bb, 0);
+  for (uint64_t bb = threadIdx.x; bb < count; bb += BS) st_relaxed(slots + bb, 0);
   return good;
 }
 
 template <class Op, class OpF, int UNROLL, int PER>
-__global__ __launch_bounds__(kRowBS, 8) void k_reduce_all_keyed(const float* __restrict__ a, uint64_t n, uint32_t grid,
+__global__ __launch_bounds__(kAllBS) void k_reduce_all_keyed(const float* __restrict__ a, uint64_t n, uint32_t grid,
                                                                 uint64_t whole_q, uint32_t whole_r, RedOut<float> out,
                                                                 FusedArgs fa) {
   using AF = typename OpF::A;
   const uint32_t b = blockIdx.x;
   if (b < grid) {
     float first = 0.0f;
-    AF acc = all_stream<OpF, float, 4, UNROLL>(a, n, grid, whole_q, whole_r, b, first);
-    acc = group_reduce<OpF, kRowBS>(acc, true);
+    AF acc = all_stream<OpF, float, 4, UNROLL, kAllBS>(a, n, grid, whole_q, whole_r, b, first);
+    acc = group_reduce<OpF, kAllBS>(acc, true);
     if (threadIdx.x == 0) publish_key(fa.slots + b, ext_key_f32<OpF>(acc));
     return;
   }
   const float a0 = a[0];  // loaded while the streaming blocks run
   uint64_t key;
-  if (fold_keys<PER>(fa.slots, grid, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
+  if (fold_keys<PER, kAllBS>(fa.slots, grid, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
     AF r = ext_unkey_f32<OpF, int64_t>(key);
     if (r.idx >= 0 && r.val == 0.0f) r.val = a[r.idx];  // the first zero's own sign
     if (is_nan(a0)) r = AF{a0, 0};  // a NaN at position 0 absorbs the whole reduction
@@ -1390,75 +1393,51 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
   return kFusedLaunched;
 }
 
-// Whole-array reduction of `n` contiguous, 16-byte aligned elements: G streaming blocks (block b
-// takes chunks b, b + G, ...) plus a combiner.  For accumulators of at most two slot words, G is
-// ceil(chunks / 2), at most kAllMaxBlocks: two 32 KB chunks per block, so that 64M f32 runs four
-// rounds of resident blocks and the dispatcher hands the later blocks to whichever CUs finish
-// first.  Block timestamps of a persistent grid of one round (1024 blocks, 8 chunks each) showed
-// why that matters: blocks with equal work took 9 to 40 us, because their shares of the
-// bandwidth differ, and half the CUs sat idle for the last 30% of the time.  A standalone sweep
-// (64M f32 sum, event-timed over back-to-back launches) gave 43.0 us for the persistent grid
-// against 40.7 us for two chunks per block, 41.8 us for four 16 KB chunks and 43.2-46.7 us for
-// one chunk of 32 or 64 KB per block.  The combiner gathers all of a lane's slots at once, so G
-// is capped by the registers that takes: 4096 blocks for one-word accumulators (f32 sum, prod,
-// mean), 2048 for two words, and the 1024-block grid for wider ones (the ordered ops' value +
-// int64 index, complex sums), whose 8 slots x 4 words would cut the occupancy.
-constexpr uint64_t kAllMaxBlocks = 4096;
+// Whole-array reduction of `n` contiguous, 16-byte aligned elements: G streaming blocks of kAllBS
+// lanes (block b takes chunks b, b + G, ...) plus a combiner block, dispatched with them.  G is
+// ceil(chunks / 2), at most 1024: 64M f32 runs one round of resident blocks, 8 chunks each, and
+// the combiner is resident from the start, polling every 128 cycles.  With 512-lane blocks of 4
+// loads per lane, a one-round grid had measured slower (43.0 us against 40.7 us for two chunks per
+// block in 4096 blocks, whose later blocks the dispatcher hands to whichever CUs finish first);
+// with 256-lane blocks of 8 loads per lane the one-round grid is the fastest measured (see kAllBS).
+constexpr uint64_t kAllMaxBlocks = 1024;  // one round of resident 256-lane blocks
 template <class Op, class OpF, class T>
 int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, const WsSplit& w, hipStream_t st) {
   constexpr int V = rvec<T>();
-  constexpr uint64_t kChunk = uint64_t(kRowBS) * 4 * V;
+  constexpr uint64_t kChunk = uint64_t(kAllBS) * kAllUnroll * V;
   constexpr uint64_t W = sizeof(typename OpF::A) / 4;
   if (n == 0 || !al16(a)) return kFusedNotCovered;
   const uint64_t nchunks = ceil_div(n, kChunk);
-  uint64_t grid = W <= 2 ? ceil_div(nchunks, uint64_t(2)) : nchunks;
-  const uint64_t max_grid = W == 1 ? kAllMaxBlocks : W == 2 ? kAllMaxBlocks / 2 : 2 * kRowBS;
-  if (grid > max_grid) grid = max_grid;
+  uint64_t grid = ceil_div(nchunks, uint64_t(2));
+  if (grid > kAllMaxBlocks) grid = kAllMaxBlocks;
   if (grid < 2) return kFusedNotCovered;
   if (grid * W * 8 > w.payload_bytes) return kFusedNoRoom;
   FusedArgs fa{};
   fa.slots = w.payload;
   fa.fault = w.fault;
   fa.spin_limit = wait_spin_limit();
-  if constexpr (Op::kOrdered && std::is_same_v<T, float>) {
-    if (n < 0xffffffffull) {  // one key per block, the grid of one-word accumulators
-      uint64_t kg = ceil_div(nchunks, uint64_t(2));
-      if (kg > kAllMaxBlocks) kg = kAllMaxBlocks;
-      if (kg >= 2 && kg * 8 <= w.payload_bytes) {
-        const uint32_t g = uint32_t(kg);
-        const uint64_t q = (n / kChunk) / kg;
-        const uint32_t r = uint32_t((n / kChunk) % kg);
-        const dim3 blocks(g + 1);
-        const uint64_t per = ceil_div(kg, uint64_t(kRowBS));
-        if (per == 1)
-          k_reduce_all_keyed<Op, OpF, 4, 1><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-        else if (per == 2)
-          k_reduce_all_keyed<Op, OpF, 4, 2><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-        else if (per <= 4)
-          k_reduce_all_keyed<Op, OpF, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-        else
-          k_reduce_all_keyed<Op, OpF, 4, 8><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-        return kFusedLaunched;
-      }
-    }
-  }
   const uint32_t g = uint32_t(grid);
   const dim3 blocks(g + 1);
   const uint64_t q = (n / kChunk) / grid;
   const uint32_t r = uint32_t((n / kChunk) % grid);
-  const uint64_t per = ceil_div(grid, uint64_t(kRowBS));
-  if (per == 1) {
-    k_reduce_all_fused<Op, OpF, T, V, 4, 1><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-  } else if (per == 2) {
-    k_reduce_all_fused<Op, OpF, T, V, 4, 2><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-  } else if constexpr (W == 1) {
-    if (per <= 4)
-      k_reduce_all_fused<Op, OpF, T, V, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-    else
-      k_reduce_all_fused<Op, OpF, T, V, 4, 8><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
-  } else if constexpr (W == 2) {
-    k_reduce_all_fused<Op, OpF, T, V, 4, 4><<<blocks, kRowBS, 0, st>>>(a, n, g, q, r, out, fa);
+  const uint64_t per = ceil_div(grid, uint64_t(kAllBS));  // combiner slots per lane, at most 4
+  if constexpr (Op::kOrdered && std::is_same_v<T, float>) {
+    if (n < 0xffffffffull) {  // one key per block
+      if (per == 1)
+        k_reduce_all_keyed<Op, OpF, kAllUnroll, 1><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
+      else if (per == 2)
+        k_reduce_all_keyed<Op, OpF, kAllUnroll, 2><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
+      else
+        k_reduce_all_keyed<Op, OpF, kAllUnroll, 4><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
+      return kFusedLaunched;
+    }
   }
+  if (per == 1)
+    k_reduce_all_fused<Op, OpF, T, V, kAllUnroll, 1><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
+  else if (per == 2)
+    k_reduce_all_fused<Op, OpF, T, V, kAllUnroll, 2><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
+  else
+    k_reduce_all_fused<Op, OpF, T, V, kAllUnroll, 4><<<blocks, kAllBS, 0, st>>>(a, n, g, q, r, out, fa);
   return kFusedLaunched;
 }
 
