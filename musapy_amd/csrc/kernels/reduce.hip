@@ -247,8 +247,14 @@ __global__ __launch_bounds__(BS) void k_reduce_row(const T* __restrict__ a, RowA
   uint64_t o = 0, t = 0, k0 = 0;
   T first{};
   if (live) {
-    o = w / ra.tiles;
-    t = w - o * ra.tiles;
+    // one tile per output (every reduction that fills the GPU with its outputs): no 64-bit
+    // division in front of the first load
+    if (ra.tiles == 1) {
+      o = w;
+    } else {
+      o = w / ra.tiles;
+      t = w - o * ra.tiles;
+    }
     int64_t off[1];
     row_offsets<1>(ra.ix, uint32_t(o), off);
     k0 = t * ra.chunk;
