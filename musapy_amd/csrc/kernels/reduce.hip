@@ -1098,6 +1098,187 @@ __global__ __launch_bounds__(kRowBS, 8) void k_reduce_rows2d_keyed(const float* 
   }
 }
 
+// max / min over both axes of a C-contiguous f32 (R, C) array whose rows are whole 32 KB chunks
+// (C a multiple of kAllChunk, at most 256 chunks per row), in the whole-array reductions' shape:
+// G <= 1024 resident 256-lane blocks, block b taking chunks b, b + G, ... (row-major order, so
+// chunk c is row c / cpr), 8 loads in flight per lane, the next chunk's loads issued while one is
+// folded, plus a combiner block.  Each lane keeps the best key over its elements (ext_key_f32 of
+// (value, column * R + row), so that ties go to the first element in column-major order, which is
+// what the reference's axis-0-then-axis-1 passes keep); a chunk is searched for its first extreme
+// only when its extreme reaches the lane's best.  Row 0 decides which columns count: the blocks
+// that hold its chunks (blocks 0 .. cpr - 1, their first chunk) publish, per wave, whether their
+// part held a NaN (in kFlag2Copies copies); every block reads them after its last chunk and, only
+// when row 0 holds a NaN, folds its chunks again with those columns masked.
+constexpr int kFlag2Copies = 16;
+constexpr uint64_t kFlag2Stride = 1024;  // words between copies: up to 256 chunks x 4 waves
+constexpr uint64_t kAllChunk = uint64_t(kAllBS) * kAllUnroll * 4;  // f32 elements per chunk
+
+template <class OpF>
+__device__ inline uint64_t chunk2d_key(uint64_t best, float (&xs)[kAllUnroll][4], const float* row0,
+                                       bool masked, uint32_t col0, uint64_t R, uint32_t r) {
+  using Op = OpExt<float, OpF::kMax, false, int32_t>;
+  float m = xs[0][0];
+  if (masked) {
+    // columns whose row-0 element is NaN do not count (row0 holds this chunk's row-0 values)
+#pragma unroll
+    for (int u = 0; u < kAllUnroll; ++u) {
+      const Vec<float, 4> h = vload<float, 4>(row0 + (u * kAllBS + threadIdx.x) * 4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (is_nan(h.v[v])) xs[u][v] = qnan<float>();
+    }
+    m = xs[0][0];
+  }
+#pragma unroll
+  for (int u = 0; u < kAllUnroll; ++u)
+#pragma unroll
+    for (int v = (u == 0 ? 1 : 0); v < 4; ++v) m = Op::pick(m, xs[u][v]);
+  if (is_nan(m)) return best;
+  // the best key m could have in this chunk (at its lowest column-major index): when it does not
+  // beat the lane's best, no element of the chunk can, and the search is skipped
+  const uint64_t top = ext_key_f32<OpF>(VI<float, int64_t>{m, int64_t(col0) * int64_t(R) + r});
+  if (top <= best) return best;
+  typename Op::A c = Op::template step_chunk<kAllUnroll, 4>(Op::init(), xs, threadIdx.x * 4, kAllBS * 4, 0);
+  const uint64_t key =
+      ext_key_f32<OpF>(VI<float, int64_t>{c.val, int64_t(col0 + uint32_t(c.idx)) * int64_t(R) + r});
+  return key > best ? key : best;
+}
+
+template <class OpF, int PER>
+__global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __restrict__ a, uint64_t R, uint32_t C,
+                                                              uint32_t grid, uint64_t whole_q, uint32_t whole_r,
+                                                              RedOut<float> out, FusedArgs fa) {
+  using AF = typename OpF::A;
+  constexpr uint32_t stepk = uint32_t(kAllBS) * 4;
+  const uint32_t cpr = C / uint32_t(kAllChunk);
+  const uint64_t nch = R * cpr;
+  uint64_t* const flags = fa.slots;  // [copy][chunk of row 0][wave]: 1 + (a NaN in that part)
+  uint64_t* const keys = fa.slots + kFlag2Copies * kFlag2Stride;
+  const uint32_t b = blockIdx.x;
+  const int wv = threadIdx.x / kWave;
+  if (b < grid) {
+    auto rowcol = [&](uint64_t c, uint32_t& r, uint32_t& col0) {
+      const uint32_t cc = uint32_t(c);  // R * C < 2^32
+      r = cpr == 1 ? cc : cc / cpr;
+      col0 = (cc - r * cpr) * uint32_t(kAllChunk);
+    };
+    Vec<float, 4> x[kAllUnroll], y[kAllUnroll];
+    auto load = [&](uint64_t c, Vec<float, 4>(&d)[kAllUnroll]) {
+      const float* p = a + c * kAllChunk + threadIdx.x * 4;
+#pragma unroll
+      for (int u = 0; u < kAllUnroll; ++u) d[u] = vload_nt<float, 4>(p + u * stepk);
+    };
+    uint64_t best = 0;
+    auto fold = [&](uint64_t c, const Vec<float, 4>(&d)[kAllUnroll], bool masked) {
+      float xs[kAllUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kAllUnroll; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xs[u][v] = d[u].v[v];
+      uint32_t r, col0;
+      rowcol(c, r, col0);
+      if (!masked && c == b && b < cpr) {
+        // a part of row 0: publish whether it holds a NaN (per wave, no barrier in the stream)
+        bool nan = false;
+#pragma unroll
+        for (int u = 0; u < kAllUnroll; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) nan = nan || is_nan(xs[u][v]);
+        const bool any = __ballot(nan) != 0;
+        if (threadIdx.x % kWave < kFlag2Copies)
+          st_relaxed(flags + (threadIdx.x % kWave) * kFlag2Stride + b * (kAllBS / kWave) + wv, any ? 2 : 1);
+      }
+      best = chunk2d_key<OpF>(best, xs, a + col0, masked, col0, R, r);
+    };
+    const uint64_t mine = whole_q + (b < whole_r ? 1 : 0);  // nch = whole_q * grid + whole_r (host)
+    // row 0's NaN flags: lane l reads flag l of this block's copy.  The first read is issued with
+    // the block's last loads, so that its round trip overlaps the last folds (the flags were
+    // published at the blocks' first chunks); a flag not yet set is polled (bounded wait; a wait
+    // that runs out counts as a NaN, so the block masks, which is always right).
+    const uint32_t nflags = cpr * (kAllBS / kWave);
+    const uint64_t* fc = flags + (b % kFlag2Copies) * kFlag2Stride;
+    uint64_t f0 = 0;  // flag threadIdx.x (the first of the lane's flags)
+    auto read_flag = [&]() {
+      if (threadIdx.x < nflags && fa.spin_limit > 0) f0 = ld_relaxed(fc + threadIdx.x);
+    };
+    if (mine > 0) {
+      uint64_t c = b;
+      load(c, x);
+      uint64_t i = 0;
+      for (; i + 2 < mine; i += 2) {
+        load(c + grid, y);
+        fold(c, x, false);
+        load(c + 2 * grid, x);
+        fold(c + grid, y, false);
+        c += 2 * grid;
+      }
+      const bool two = i + 1 < mine;
+      if (two) load(c + grid, y);
+      read_flag();
+      fold(c, x, false);
+      if (two) fold(c + grid, y, false);
+    } else {
+      read_flag();
+    }
+    bool nan0 = false;
+    for (uint32_t l = threadIdx.x; l < nflags; l += kAllBS) {
+      uint64_t f = l == threadIdx.x ? f0 : (fa.spin_limit > 0 ? ld_relaxed(fc + l) : 0);
+      for (uint32_t spins = 1; f == 0 && spins < fa.spin_limit; ++spins) {
+        __builtin_amdgcn_s_sleep(2);
+        f = ld_relaxed(fc + l);
+      }
+      nan0 = nan0 || f != 1;
+    }
+    if (__syncthreads_or(nan0 ? 1 : 0)) {  // row 0 holds a NaN: fold the chunks again, masked
+      best = 0;
+      for (uint64_t c = b; c < nch; c += grid) {
+        load(c, x);
+        fold(c, x, true);
+      }
+    }
+    // block max of the lanes' keys
+#pragma unroll
+    for (int m = kWave / 2; m >= 1; m >>= 1) {
+      const uint64_t o = acc_shfl(best, m);
+      best = o > best ? o : best;
+    }
+    __shared__ uint64_t part[kAllBS / kWave];
+    if (threadIdx.x % kWave == 0) part[wv] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 1; i < kAllBS / kWave; ++i) best = part[i] > best ? part[i] : best;
+      publish_key(keys + b, best);
+    }
+    return;
+  }
+  // combiner
+  const float a0 = a[0];
+  uint64_t key;
+  if (fold_keys<PER, kAllBS>(keys, grid, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
+    AF r = ext_unkey_f32<OpF, int64_t>(key);
+    if (r.idx >= 0 && r.val == 0.0f) {  // the first zero's own sign
+      const uint64_t col = uint64_t(r.idx) / R, rw = uint64_t(r.idx) % R;
+      r.val = a[rw * uint64_t(C) + col];
+    }
+    if (is_nan(a0)) r = AF{a0, 0};  // column 0 is NaN: it absorbs the second pass
+    write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
+  }
+  // every block has read the flags (its key is published): return them to zero, each once seen
+  // set (a zero stored unseen could land before the flag store it should clear)
+  const uint32_t nflags = cpr * (kAllBS / kWave);
+  for (uint32_t i = threadIdx.x; i < nflags * kFlag2Copies; i += kAllBS) {
+    uint64_t* p = flags + (i / nflags) * kFlag2Stride + (i % nflags);
+    uint64_t f = ld_relaxed(p);
+    for (uint32_t spins = 1; f == 0 && spins < fa.spin_limit; ++spins) {
+      __builtin_amdgcn_s_sleep(2);
+      f = ld_relaxed(p);
+    }
+    if (f == 0) atomicOr(fa.fault, kFaultReduceWait);  // reported: the caller zeroes the workspace again
+    st_relaxed(p, 0);
+  }
+}
+
 // --------------------------------------------------------------------------------------------
 // pair kernel (arg final / mid): rows of (value, index) partials, contiguous [out][n]
 template <class Op, class T, int GROUP, int WRITE>
@@ -1460,6 +1641,28 @@ int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, 
   if (R == 0 || C == 0 || !ws_split(ws, ws_bytes, w) || R >= (uint64_t(1) << 31) || R * C >= (uint64_t(1) << 62))
     return kFusedNotCovered;
   if constexpr (std::is_same_v<T, float>) {
+    // rows of whole 32 KB chunks: the chunked kernel in one round of resident blocks
+    const uint64_t cpr = C / kAllChunk;
+    if (C % kAllChunk == 0 && cpr <= 256 && R * C < 0xffffffffull && al16(a) &&
+        (kFlag2Copies * kFlag2Stride + kAllMaxBlocks) * 8 <= w.payload_bytes) {
+      FusedArgs fk{};
+      fk.slots = w.payload;
+      fk.fault = w.fault;
+      fk.spin_limit = wait_spin_limit();
+      const uint64_t nch = R * cpr;
+      const uint32_t grid = uint32_t(nch < kAllMaxBlocks ? nch : kAllMaxBlocks);
+      const dim3 g(grid + 1);
+      const uint64_t per = ceil_div(grid, uint64_t(kAllBS));
+      const uint64_t q = nch / grid;
+      const uint32_t rr = uint32_t(nch % grid);
+      if (per == 1)
+        k_reduce_2d_chunks<OpF, 1><<<g, kAllBS, 0, st>>>(a, R, uint32_t(C), grid, q, rr, out, fk);
+      else if (per == 2)
+        k_reduce_2d_chunks<OpF, 2><<<g, kAllBS, 0, st>>>(a, R, uint32_t(C), grid, q, rr, out, fk);
+      else
+        k_reduce_2d_chunks<OpF, 4><<<g, kAllBS, 0, st>>>(a, R, uint32_t(C), grid, q, rr, out, fk);
+      return kFusedLaunched;
+    }
     // rows of at least one block round: the row-keyed kernel
     if (C >= 2048 && C % 4 == 0 && C < (uint64_t(1) << 31) && R * C < 0xffffffffull && al16(a) &&
         (64 * 32 + R) * 8 <= w.payload_bytes) {

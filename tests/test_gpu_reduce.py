@@ -465,6 +465,38 @@ def test_two_axis_single_launch(kind, dt):
         check_reduce(kind, y, (0, 1))
 
 
+@pytest.mark.parametrize("kind", ["max", "min"])
+def test_two_axis_chunked_rows(kind):
+    """f32 rows of whole 8192-element chunks take the chunked two-axis kernel (one round of up to
+    1024 blocks, chunk c = row c / chunks-per-row): grids smaller than the chunk count and larger,
+    several chunks per row, row 0's NaN in a later chunk (its block masks every block's refold),
+    ties across rows and columns resolved in column-major order, infinities, a column of NaNs
+    below row 0."""
+    sign = 1 if kind == "max" else -1
+    for shape in ((1, 8192), (3, 8192), (100, 16384), (2049, 8192), (64, 32768), (1031, 16384)):
+        R, C = shape
+        x = RNG.standard_normal(shape).astype(np.float32)
+        check_reduce(kind, x, (0, 1))
+        t = x.copy()                       # the extreme twice: column-major order picks the left one
+        t[R - 1, 7] = sign * 50.0
+        t[0, 8] = sign * 50.0
+        check_reduce(kind, t, (0, 1))
+        if R > 1:
+            t[R // 2, 7] = sign * 50.0     # same column, earlier row
+            check_reduce(kind, t, (0, 1))
+        y = x.copy()
+        y[0, C - 3] = np.nan               # row 0's NaN in its last chunk drops column C - 3 ...
+        y[R - 1, C - 3] = sign * np.inf    # ... and the infinity below it
+        y[R // 2, 1:9] = np.nan            # skipped
+        check_reduce(kind, y, (0, 1))
+        y[R - 1, 2] = sign * np.inf        # an eligible infinity wins
+        check_reduce(kind, y, (0, 1))
+        z = np.full(shape, -sign, np.float32)
+        z[0, C - 1] = -0.0
+        z[R - 1, 1] = 0.0
+        check_reduce(kind, z, (0, 1))
+
+
 @pytest.mark.parametrize("kind", ["max", "min", "argmax", "argmin"])
 def test_whole_array_signed_zero_ties(kind):
     """Whole-array f32 reductions of 3M+ elements (the persistent grid with its packed-key wave

@@ -100,14 +100,19 @@ def test_column_reduction_gives_up_and_recovers():
 
 
 def test_two_axis_reduction_gives_up_and_recovers():
-    """max / min over (0, 1) in one launch (row-keyed kernel, 3000 rows): the combiner finds no row
-    key published, and the row blocks after the first resident generation find no flag from block
-    0 and fold their rows masked instead (always right).  Row 0 with and without a NaN head."""
+    """max / min over (0, 1) in one launch (row-keyed kernel, 3000 rows; chunked kernel, 600 rows of
+    8192): the combiner finds no key published, and the blocks that wait for row 0's flags find none
+    and fold their rows masked instead (always right).  Row 0 with and without a NaN head."""
     x = RNG.standard_normal((3000, 2048)).astype(np.float32)
     y = x.copy()
     y[0, 3] = np.nan  # drops column 3, whatever it holds below
     y[2999, 3] = 1e30
-    for arr in (x, y):
+    # rows of whole 8192-element chunks: the chunked kernel (its row-0 flags and keys time out)
+    u = RNG.standard_normal((600, 8192)).astype(np.float32)
+    v = u.copy()
+    v[0, 8000] = np.nan
+    v[599, 8000] = 1e30
+    for arr in (x, y, u, v):
         for op in ("max", "min"):
             _fresh_stream_case(lambda arr=arr: (ms.from_numpy(arr),), lambda X, op=op: getattr(ms, op)(X, axis=(0, 1)),
                                lambda got, what, arr=arr, op=op: assert_bits_equal(got, R.reduce(arr, op, (0, 1)), what))
