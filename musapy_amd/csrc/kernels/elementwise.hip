@@ -318,7 +318,9 @@ template <class TI, int PL> constexpr int tr_tp() { return PL * tr_vec<TI>(); }
 // (8192, 4096) view and not kept: the functor applied on the store side (LDS holding the input),
 // exp 52.6 against 51.6 us; software-pipelined blocks of 2-4 tiles (next tile's loads in flight,
 // LDS-only barriers), 52.3-56 us; the block -> tile map grouped by XCD, level; 16 lanes x 256 rows
-// (50.3 us, but X^T 97.3 us) and 8 x 512, 16 x 256 in 512 lanes, 32 x 128 in 512 lanes (53-55 us).
+// (50.3 us, but X^T 97.3 us) and 8 x 512, 16 x 256 in 512 lanes, 32 x 128 in 512 lanes (53-55 us);
+// XOR-swizzled tile columns, free of LDS bank conflicts (which take 3/4 of this tile's LDS-active
+// cycles), 50.7-53.7 against 50.0 us, X^T 94-104 against 91.7 us.
 template <class F> struct tr_moves_only : std::false_type {};  // copies and casts
 template <> struct tr_moves_only<IdentityF> : std::true_type {};
 template <class S, class D> struct tr_moves_only<CastF<S, D>> : std::true_type {};

@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
 
 // --------------------------------------------------------------------------------------------
 // Whole-array reduction (one output): block b of G streams chunks b, b+G, b+2G, ... (chunk =
-// one round of the block, 512 lanes x UNROLL x 16 bytes; G from launch_reduce_all_fused), folding
+// one round of the block, kAllBS lanes x UNROLL x 16 bytes; G from launch_reduce_all_fused), folding
 // each chunk into its lanes' running accumulators in that fixed order; then blocks publish and a
 // combiner block (index G) folds the G block results as in k_reduce_row_fused.  Ordered ops fold
 // a chunk with tile-relative int32 indices and move it into an int64 running accumulator per lane.
@@ -1629,9 +1629,11 @@ int launch_reduce_all_fused(const T* a, RedOut<T> out, uint64_t n, const WsSplit
 }
 
 
-// max / min over both axes of a C-contiguous (R, C) array in one launch: f32 rows of at least
-// 2048 elements as keyed rows (k_reduce_rows2d_keyed, R + 1 blocks), the rest with the column
-// kernel's tiling (k_reduce_col2d, about 256 blocks); kFusedNotCovered when the shape fits neither
+// max / min over both axes of a C-contiguous (R, C) array in one launch: f32 rows of whole 32 KB
+// chunks in the whole-array grid (k_reduce_2d_chunks, at most 1024 + 1 blocks), other f32 rows of
+// at least 2048 elements as keyed rows (k_reduce_rows2d_keyed, R + 1 blocks), the rest with the
+// column kernel's tiling (k_reduce_col2d, about 256 blocks); kFusedNotCovered when the shape fits
+// none of them
 template <class Op, class OpF, class T>
 int launch_reduce_2d_ordered(const T* a, RedOut<T> out, uint64_t R, uint64_t C, void* ws, size_t ws_bytes,
                              hipStream_t st) {
