@@ -32,6 +32,11 @@ constexpr int kRowBS = 512;  // block size of the block-per-segment row kernel (
 // took the dispatcher about 3.6 us to start.
 constexpr int kAllBS = 256;
 constexpr int kAllUnroll = 8;
+// Chunks of loads held per lane (walk_chunks): kAllBuffers - 1 chunks in flight at each fold.  With
+// the same registers, 4 buffers of 4 loads (12 in flight at each fold) and 3 of 4 measured no faster
+// than 2 of 8 (64M f32 sum, argmax and max over (0,1) within 0.5 us, 256M level): the folds are not
+// what holds the stream back.
+constexpr int kAllBuffers = 2;
 
 // what a kernel writes per (output, tile)
 enum : int { kWriteFinal = 0, kWriteVal = 1, kWritePair = 2 };
@@ -407,6 +412,45 @@ __global__ __launch_bounds__(kRowBS) void k_reduce_row_fused(const T* __restrict
 // combiner block (index G) folds the G block results as in k_reduce_row_fused.  Ordered ops fold
 // a chunk with tile-relative int32 indices and move it into an int64 running accumulator per lane.
 //
+// Walks a block's chunks k = 0 .. mine - 1 through NB register buffers: chunk k lives in buffer
+// k % NB, and the loads of chunks k + 1 .. k + NB - 1 are in flight while chunk k is folded.  The
+// buffer of every load and fold is a compile-time index (the steady loop is unrolled NB times and
+// the last NB - 1 .. 2NB - 2 chunks take one of NB straight-line tails), so no registers are copied
+// and no prefetch is conditional: a conditional load would make the wait before each later fold
+// cover it too.  `last()` runs once, after the last chunk's loads are issued and before the folds
+// that follow them.
+template <int NB, class B, class Load, class Fold, class Last>
+__device__ inline void walk_chunks(uint64_t mine, B (&buf)[NB], Load&& load, Fold&& fold, Last&& last) {
+  static_assert(NB >= 2, "at least two buffers");
+  if (mine < uint64_t(NB - 1)) {  // fewer chunks than a full prefetch: all loads, then the folds
+    static_for<NB - 1>([&](auto J) { if (J.value < mine) load(uint64_t(J.value), buf[J.value]); });
+    last();
+    static_for<NB - 1>([&](auto J) { if (J.value < mine) fold(uint64_t(J.value), buf[J.value]); });
+    return;
+  }
+  static_for<NB - 1>([&](auto J) { load(uint64_t(J.value), buf[J.value]); });
+  uint64_t k = 0;
+  for (; k + 2 * NB - 1 <= mine; k += NB) {
+    static_for<NB>([&](auto J) {
+      load(k + J.value + NB - 1, buf[(J.value + NB - 1) % NB]);
+      fold(k + J.value, buf[J.value]);
+    });
+  }
+  // mine - k = NB - 1 + e chunks are left, 0 <= e < NB; chunks k .. k + NB - 2 are loaded
+  const uint32_t e = uint32_t(mine - k) - uint32_t(NB - 1);
+  static_for<NB>([&](auto E) {
+    if (e == E.value) {
+      if constexpr (E.value == 0) last();
+      static_for<E.value>([&](auto J) {
+        load(k + J.value + NB - 1, buf[(J.value + NB - 1) % NB]);
+        if constexpr (J.value + 1 == E.value) last();
+        fold(k + J.value, buf[J.value]);
+      });
+      static_for<NB - 1>([&](auto J) { fold(k + E.value + J.value, buf[(E.value + J.value) % NB]); });
+    }
+  });
+}
+
 // One streaming block's lane accumulator (before the block reduction); `first` receives element 0
 // on lane 0 of the block that reads it.
 template <class OpF, class T, int VEC, int UNROLL, int BS>
@@ -417,17 +461,18 @@ __device__ inline typename OpF::A all_stream(const T* __restrict__ a, uint64_t n
   AF acc = OpF::init();
   // The lane's running accumulator (absolute int64 indices) continues from chunk to chunk, so
   // an ordered fold searches a chunk only when the chunk beats it.  Whole chunks are software
-  // pipelined: the next chunk's loads are in flight while the current one is folded.
+  // pipelined: the next kAllBuffers - 1 chunks' loads are in flight while one is folded.
   constexpr uint32_t stepk = uint32_t(BS) * VEC;
   const uint64_t whole = n / kChunk;
-  uint64_t c = b;
-  Vec<T, VEC> x[UNROLL], y[UNROLL];  // ping-pong buffers: no register copies between chunks
-  auto load = [&](uint64_t cc, Vec<T, VEC>(&dst)[UNROLL]) {
-    const T* p = a + cc * kChunk + threadIdx.x * VEC;
+  Vec<T, VEC> buf[kAllBuffers][UNROLL];
+  // the block's k-th chunk is chunk b + k * grid of the array
+  auto load = [&](uint64_t k, Vec<T, VEC>(&dst)[UNROLL]) {
+    const T* p = a + (b + k * grid) * kChunk + threadIdx.x * VEC;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) dst[u] = vload_nt<T, VEC>(p + u * stepk);
   };
-  auto fold = [&](uint64_t cc, const Vec<T, VEC>(&src)[UNROLL]) {
+  auto fold = [&](uint64_t k, const Vec<T, VEC>(&src)[UNROLL]) {
+    const uint64_t cc = b + k * grid;
     T xs[UNROLL][VEC];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
@@ -436,30 +481,11 @@ __device__ inline typename OpF::A all_stream(const T* __restrict__ a, uint64_t n
     if (cc == 0) first = xs[0][0];  // lane 0 holds element 0
     acc = OpF::template step_chunk<UNROLL, VEC>(acc, xs, threadIdx.x * VEC, stepk, int64_t(cc * kChunk));
   };
-  // the steady-state loop prefetches unconditionally (a conditional prefetch would make the
-  // wait before each fold cover the prefetch too); the last one or two chunks are peeled.
   // whole = whole_q * grid + whole_r (from the host: a 64-bit division here would delay every
   // block's first load)
   const uint64_t mine = whole_q + (b < whole_r ? 1 : 0);  // whole chunks of this block
-  if (mine > 0) {
-    load(c, x);
-    uint64_t i = 0;
-    for (; i + 2 < mine; i += 2) {
-      load(c + grid, y);
-      fold(c, x);
-      load(c + 2 * grid, x);
-      fold(c + grid, y);
-      c += 2 * grid;
-    }
-    // one or two chunks left.  Written as a conditional load followed by the folds, not as two
-    // branches that both start with fold(c, x): the compiler hoisted that common start above
-    // the branch, so the second chunk's loads waited for the first chunk's data.
-    const bool two = i + 1 < mine;
-    if (two) load(c + grid, y);
-    fold(c, x);
-    if (two) fold(c + grid, y);
-    c = b + mine * grid;  // the first chunk index past this block's whole chunks
-  }
+  walk_chunks(mine, buf, load, fold, [] {});
+  const uint64_t c = b + mine * grid;  // the first chunk index past this block's whole chunks
   if (c == whole && whole * kChunk < n) {  // the last, partial chunk
     T f{};
     acc = accumulate_segment<OpF, T, BS, VEC, UNROLL>(a + c * kChunk, uint32_t(n - c * kChunk), threadIdx.x, 1,
@@ -1162,7 +1188,7 @@ __global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __rest
       r = cpr == 1 ? cc : cc / cpr;
       col0 = (cc - r * cpr) * uint32_t(kAllChunk);
     };
-    Vec<float, 4> x[kAllUnroll], y[kAllUnroll];
+    Vec<float, 4> buf[kAllBuffers][kAllUnroll];
     auto load = [&](uint64_t c, Vec<float, 4>(&d)[kAllUnroll]) {
       const float* p = a + c * kAllChunk + threadIdx.x * 4;
 #pragma unroll
@@ -1201,25 +1227,10 @@ __global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __rest
     auto read_flag = [&]() {
       if (threadIdx.x < nflags && fa.spin_limit > 0) f0 = ld_relaxed(fc + threadIdx.x);
     };
-    if (mine > 0) {
-      uint64_t c = b;
-      load(c, x);
-      uint64_t i = 0;
-      for (; i + 2 < mine; i += 2) {
-        load(c + grid, y);
-        fold(c, x, false);
-        load(c + 2 * grid, x);
-        fold(c + grid, y, false);
-        c += 2 * grid;
-      }
-      const bool two = i + 1 < mine;
-      if (two) load(c + grid, y);
-      read_flag();
-      fold(c, x, false);
-      if (two) fold(c + grid, y, false);
-    } else {
-      read_flag();
-    }
+    // the block's k-th chunk is chunk b + k * grid of the array
+    walk_chunks(
+        mine, buf, [&](uint64_t k, Vec<float, 4>(&d)[kAllUnroll]) { load(b + k * grid, d); },
+        [&](uint64_t k, const Vec<float, 4>(&d)[kAllUnroll]) { fold(b + k * grid, d, false); }, read_flag);
     bool nan0 = false;
     for (uint32_t l = threadIdx.x; l < nflags; l += kAllBS) {
       uint64_t f = l == threadIdx.x ? f0 : (fa.spin_limit > 0 ? ld_relaxed(fc + l) : 0);
@@ -1232,8 +1243,8 @@ __global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __rest
     if (__syncthreads_or(nan0 ? 1 : 0)) {  // row 0 holds a NaN: fold the chunks again, masked
       best = 0;
       for (uint64_t c = b; c < nch; c += grid) {
-        load(c, x);
-        fold(c, x, true);
+        load(c, buf[0]);
+        fold(c, buf[0], true);
       }
     }
     // block max of the lanes' keys
