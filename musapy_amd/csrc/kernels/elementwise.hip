@@ -23,11 +23,15 @@ namespace mpy {
 
 constexpr int kBlock = 256;
 // Lanes per block of the flat kernels (unit-stride operands, one vector per lane).  Measured on
-// MI355X with streaming stores: binary ops run faster in 128-lane blocks (64M f32 add 124.2 ->
-// 119.4 us, c128 mul 124.4 -> 119.7, the i64 + f64 add 62.5 -> 60.1, 16M f32 add 33.4 -> 32.9),
-// unary ops and casts slower (clamp of 16M f64 43.3 -> 44.1, f64 -> f32 34.1 -> 34.6).
+// MI355X with streaming stores: binary ops run faster in 128-lane blocks than in 256 (64M f32 add
+// 124.2 -> 119.4 us, c128 mul 124.4 -> 119.7, the i64 + f64 add 62.5 -> 60.1, 16M f32 add 33.4
+// -> 32.9), unary ops and casts slower (clamp of 16M f64 43.3 -> 44.1, f64 -> f32 34.1 -> 34.6).
+// Same-type binary ops run faster still in 64-lane blocks (event-timed, one A/B run: 16M f32 add
+// 32.7-32.8 -> 32.1-32.3 us, 64M 123.6-124.0 -> 122.4-122.6, c128 mul 123.9-124.4 -> 122.8-123.0),
+// the fused-promotion kernel slower (the i64 + f64 add 61.9-62.0 -> 62.7-63.4), so it keeps 128.
 constexpr int kFlatBlockUnary = 256;
-constexpr int kFlatBlockBinary = 128;
+constexpr int kFlatBlockBinary = 64;
+constexpr int kFlatBlockMixed = 128;
 
 // ---------------------------------------------------------------------------------------------
 // operand access modes
@@ -210,10 +214,10 @@ __global__ __launch_bounds__(kBlock) void k_binary_rows(In<T> a, int64_t sa, In<
 // mixed dtypes: c = f(TC(a), TC(b)) with the cast functors of the cast kernels, i.e. exactly the
 // reference's cast-then-compute (op_builder.rs:410-417) without materialising the cast.
 template <int VEC, bool NTS, class F, class TC, class TA, class TB>
-__global__ __launch_bounds__(kFlatBlockBinary) void k_binary_flat_mixed(const TA* __restrict__ a,
+__global__ __launch_bounds__(kFlatBlockMixed) void k_binary_flat_mixed(const TA* __restrict__ a,
                                                                         const TB* __restrict__ b,
                                                               TC* __restrict__ c, uint64_t n, bool nt, F f) {
-  const uint64_t i0 = (uint64_t(blockIdx.x) * kFlatBlockBinary + threadIdx.x) * VEC;
+  const uint64_t i0 = (uint64_t(blockIdx.x) * kFlatBlockMixed + threadIdx.x) * VEC;
   const CastF<TA, TC> ca{};
   const CastF<TB, TC> cb{};
   if (i0 + VEC <= n) {
@@ -744,11 +748,11 @@ void launch_binary_mixed(const void* a, const void* b, void* c, int ndim, const 
   constexpr int V = 16 / (sizeof(TA) > sizeof(TB) ? (sizeof(TA) > sizeof(TC) ? sizeof(TA) : sizeof(TC))
                                                   : (sizeof(TB) > sizeof(TC) ? sizeof(TB) : sizeof(TC)));
   if (p.ndim == 1 && p.stride[1][0] == 1 && p.stride[2][0] == 1 && aligned16(a) && aligned16(b) && aligned16(c)) {
-    const uint64_t blocks = (p.numel + uint64_t(kFlatBlockBinary) * V - 1) / (uint64_t(kFlatBlockBinary) * V);
+    const uint64_t blocks = (p.numel + uint64_t(kFlatBlockMixed) * V - 1) / (uint64_t(kFlatBlockMixed) * V);
     const bool nt = p.numel * (sizeof(TA) + sizeof(TB)) >= kStreamLoadBytes;
     const bool nts = p.numel * sizeof(TC) >= kStreamStoreBytes;
     with_store_policy(nts, [&](auto NT) {
-      k_binary_flat_mixed<V, NT.value, F, TC, TA, TB><<<dim3(unsigned(blocks)), kFlatBlockBinary, 0, st>>>(
+      k_binary_flat_mixed<V, NT.value, F, TC, TA, TB><<<dim3(unsigned(blocks)), kFlatBlockMixed, 0, st>>>(
           pa, pb, pc, p.numel, nt, f);
     });
     return;
