@@ -1265,6 +1265,20 @@ __global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __rest
   }
   // combiner
   const float a0 = a[0];
+  // Row 0's NaN flags are set at their blocks' first chunks, long before the last key: they are
+  // read here, while the streaming blocks run, and returned to zero with plain stores once every
+  // block has read them (after the keys), so no read is left after the result write.  A flag is
+  // cleared only once seen set: a zero stored unseen could land before the flag store it clears.
+  const uint32_t nflags = cpr * (kAllBS / kWave);
+  for (uint32_t i = threadIdx.x; i < nflags * kFlag2Copies; i += kAllBS) {
+    const uint64_t* p = flags + (i / nflags) * kFlag2Stride + (i % nflags);
+    uint64_t f = ld_relaxed(p);
+    for (uint32_t spins = 1; f == 0 && spins < fa.spin_limit; ++spins) {
+      __builtin_amdgcn_s_sleep(2);
+      f = ld_relaxed(p);
+    }
+    if (f == 0) atomicOr(fa.fault, kFaultReduceWait);  // reported: the caller zeroes the workspace again
+  }
   uint64_t key;
   if (fold_keys<PER, kAllBS>(keys, grid, fa.spin_limit, fa.fault, key) && threadIdx.x == 0) {
     AF r = ext_unkey_f32<OpF, int64_t>(key);
@@ -1275,19 +1289,8 @@ __global__ __launch_bounds__(kAllBS) void k_reduce_2d_chunks(const float* __rest
     if (is_nan(a0)) r = AF{a0, 0};  // column 0 is NaN: it absorbs the second pass
     write_result<OpF, float, kWriteFinal>(out, 0, r, 0);
   }
-  // every block has read the flags (its key is published): return them to zero, each once seen
-  // set (a zero stored unseen could land before the flag store it should clear)
-  const uint32_t nflags = cpr * (kAllBS / kWave);
-  for (uint32_t i = threadIdx.x; i < nflags * kFlag2Copies; i += kAllBS) {
-    uint64_t* p = flags + (i / nflags) * kFlag2Stride + (i % nflags);
-    uint64_t f = ld_relaxed(p);
-    for (uint32_t spins = 1; f == 0 && spins < fa.spin_limit; ++spins) {
-      __builtin_amdgcn_s_sleep(2);
-      f = ld_relaxed(p);
-    }
-    if (f == 0) atomicOr(fa.fault, kFaultReduceWait);  // reported: the caller zeroes the workspace again
-    st_relaxed(p, 0);
-  }
+  for (uint32_t i = threadIdx.x; i < nflags * kFlag2Copies; i += kAllBS)
+    st_relaxed(flags + (i / nflags) * kFlag2Stride + (i % nflags), 0);
 }
 
 // --------------------------------------------------------------------------------------------
