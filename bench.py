@@ -237,6 +237,7 @@ def all_config_ops(ms, host_legs=False):
 
         def g(i):
             ring[i % k] = fn(i)
+        g.ring = k
         return g, nbytes, cpu
 
     def b_add64():
@@ -673,7 +674,10 @@ def main():
             fn, bytes_, cpu = build()
             row = {"op": name, "key": key}
             if fn is not None:
-                for i in range(8):  # fill the output ring and the memory pool before timing
+                # fill the output ring and the memory pool before timing: the ring holds k results, so
+                # the pool reaches its k + 1 blocks per row only at launch k + 1 (with 8 warm-up launches,
+                # the first row of a new size class with k = 8 paid a hipMalloc inside its timed loop)
+                for i in range(max(8, 2 * getattr(fn, "ring", 0))):
                     fn(i)
                 ms.synchronize()
                 t = timer.run([(lambda i=i, fn=fn: fn(i)) for i in range(20)])
