@@ -497,6 +497,32 @@ def test_two_axis_chunked_rows(kind):
         check_reduce(kind, z, (0, 1))
 
 
+@pytest.mark.parametrize("m", [3, 4, 5])
+def test_whole_array_chunk_walk(m):
+    """Whole-array f32 reductions whose 1024 streaming blocks take m or m + 1 chunks of 8192
+    elements each (the chunk walker's steady loop and both of its tails), with and without whole
+    chunks left over and a partial last chunk: sums within the bound, exact arg results, with
+    the extreme planted in the partial chunk and tied in an earlier block; and max / min over
+    both axes of m * 1024 + 5 rows of one chunk (the chunked two-axis kernel)."""
+    chunk, grid = 8192, 1024
+    for extra in (0, 517 * chunk + 1234, (grid - 1) * chunk + 8191):
+        n = m * grid * chunk + extra
+        x = RNG.standard_normal(n).astype(np.float32)
+        gx = dev(x)
+        for kind in ("sum", "argmax", "min"):
+            check_reduce(kind, x, None, gpu_x=gx)
+        y = x.copy()
+        y[n - 1] = 40.0                        # the partial chunk (or the last block's last chunk)
+        y[(m - 1) * grid * chunk + 3 * chunk + 5] = 40.0  # a tie in block 3's m-th chunk: the lower index wins
+        check_reduce("argmax", y, None)
+        check_reduce("max", y, None)
+    # the chunked two-axis kernel walks its chunks the same way: m * 1024 + 5 rows of one chunk
+    x2 = RNG.standard_normal((m * grid + 5, chunk)).astype(np.float32)
+    x2[m * grid + 4, 17] = 40.0  # in the last row: a block with m + 1 chunks
+    for kind in ("max", "min"):
+        check_reduce(kind, x2, (0, 1))
+
+
 @pytest.mark.parametrize("kind", ["max", "min", "argmax", "argmin"])
 def test_whole_array_signed_zero_ties(kind):
     """Whole-array f32 reductions of 3M+ elements (the persistent grid with its packed-key wave
