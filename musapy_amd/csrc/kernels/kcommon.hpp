@@ -137,10 +137,13 @@ __device__ inline Vec<T, N> vload_pol(const T* p, bool nt) {
 // the i64 + f64 add of 16M 66.5 -> 61.5, c128 mul 129 -> 121, the (8192, 8192) f32 transpose
 // 113 -> 107, a flip 97.5 -> 91.5, the c128 transpose 110.5 -> 102.5, C5's cumsum 195 -> 188,
 // C2's broadcast add 24.7 -> 23.1, 16M f32 add 33.6 -> 32.3 us (with 128-lane blocks).  Unary
-// ops with a 64 MB output measured slower streamed (f64 -> f32 of 16M 34.2 against 33.3 us, c64
-// abs 34.0 against 33.2), so they stream from 128 MB (clamp of 16M f64: 44.7 -> 42.7 us).
+// ops and casts stream from 32 MB: with every launch writing lines that the Infinity Cache no
+// longer holds (outputs rotated over 512 MB or more), f64 -> f32 of 16M 35.7-35.8 -> 34.3 us, c64
+// abs 35.7-36.3 -> 34.2-34.4, f32 -> bf16 18.8 -> 18.4, f32 -> f16 18.8-19.0 -> 18.5 (clamp of 16M
+// f64 level).  With outputs rotated over fewer buffers, whose writes the cache absorbed, a 64 MB
+// unary output had measured slower streamed.
 constexpr uint64_t kStreamStoreBytes = uint64_t(64) << 20;
-constexpr uint64_t kStreamStoreBytesUnary = uint64_t(128) << 20;
+constexpr uint64_t kStreamStoreBytesUnary = uint64_t(32) << 20;
 // The store policy is a template parameter, not a runtime flag: the compiler merges a runtime
 // choice between a streaming and a default store of the same value to the same address into one
 // default store (the two branches are combined and the nontemporal hint is dropped), which left
