@@ -240,7 +240,8 @@ __global__ __launch_bounds__(kFlatBlockMixed) void k_binary_flat_mixed(const TA*
 // us).  A lane loads its U items of both operands first (an operand that is row-invariant or one
 // value per row hits the cache), then computes and stores them.  Block shape, measured on MI355X
 // for C2 with streaming stores (kernel time): 512 lanes x 2 pieces 22.4 us, 256 x 2 23.4, 128 x 2
-// 22.7, 1024 x 2 24.8, 256 x 4 23.8, one piece per block 27.5.
+// 22.7, 1024 x 2 24.8, 256 x 4 23.8, one piece per block 27.5; event-timed in a later A/B, 512 x 2
+// 21.5-21.7 us, 64 x 4 22.8, 128 x 4 24.3-24.5, 64 x 8 25.2-25.4.
 constexpr int kPieceBlock = 512;  // lanes per row-pieces block
 constexpr int kPieces = 2;        // consecutive pieces per block
 struct RowPieceArgs {
