@@ -1595,9 +1595,11 @@ int launch_reduce_fused(const T* a, RedOut<T> out, int ndim, const size_t* shape
 }
 
 // Whole-array reduction of `n` contiguous, 16-byte aligned elements: G streaming blocks of kAllBS
-// lanes (block b takes chunks b, b + G, ...) plus a combiner block, dispatched with them.  G is
-// ceil(chunks / 2), at most 1024: 64M f32 runs one round of resident blocks, 8 chunks each, and
-// the combiner is resident from the start, polling every 128 cycles.  With 512-lane blocks of 4
+// lanes (block b takes chunks b, b + G, ...) plus a combiner block, dispatched after them.  G is
+// ceil(chunks / 2), at most 1024: 64M f32 runs one round of resident blocks, 8 chunks each.  The
+// sums fit five blocks per CU, so their combiner is resident from the start; the keyed arg kernels
+// (four per CU) fill the GPU with the streaming blocks, and their combiner starts when the first
+// streaming block ends, long before the last.  The combiner polls every 128 cycles.  With 512-lane blocks of 4
 // loads per lane, a one-round grid had measured slower (43.0 us against 40.7 us for two chunks per
 // block in 4096 blocks, whose later blocks the dispatcher hands to whichever CUs finish first);
 // with 256-lane blocks of 8 loads per lane the one-round grid is the fastest measured (see kAllBS).
