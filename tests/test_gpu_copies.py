@@ -96,7 +96,8 @@ def test_contiguous_reference_known_answers():
 def test_transposed_casts_every_tile_shape(shape):
     """Casts and unary ops of transposed views go through the LDS tile: 128 rows in 1024 lanes for
     casts (halved until the tile fits, 32 rows for a 1-byte input widened to 8 bytes), 64 rows in
-    512 lanes for other functors, 8 or 16 lanes along a short P.  Ragged edges on both dims."""
+    512 lanes for other functors, 8 or 16 lanes along a short P, 64 x 64 tiles for 16-byte copies.
+    Ragged edges on both dims."""
     casts = [(np.uint8, "f64"), (np.int8, "f32"), (np.int16, "i64"), (np.uint32, "f64"), (np.float32, "f64"),
              (np.float64, "f32"), (np.int64, "f32"), (np.float32, "c64"), (np.float64, "c128")]
     for src, dst in casts:
@@ -108,6 +109,10 @@ def test_transposed_casts_every_tile_shape(shape):
     assert e.shape == x.T.shape and ulp_diff_f32(e, R.unary("exp", x.T)).max() <= 2, f"exp T {shape}"
     h = rand(shape, np.float16)
     check(ms.contiguous(ms.transpose(ms.from_numpy(h))), R.contiguous(h.T), f"f16 T {shape}")
+    # 16-byte elements take 64 x 64 tiles once P reaches 64, in both tile orders (L > P: (1030, 70))
+    for dt in (np.complex64, np.complex128):
+        z = rand(shape, dt)
+        check(ms.contiguous(ms.transpose(ms.from_numpy(z))), R.contiguous(z.T), f"{np.dtype(dt).name} T {shape}")
 
 
 def test_contiguous_large_transpose_and_sizes():
