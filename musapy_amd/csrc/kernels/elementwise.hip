@@ -524,8 +524,9 @@ __global__ __launch_bounds__(kBlock) void k_binary_generic_mixed(const TA* __res
 // ---------------------------------------------------------------------------------------------
 // host side: variant selection
 // vectors per thread: one 16-byte vector per operand per thread (many short blocks) measured best
-// for the flat path on MI355X (6.7 TB/s add at 16M elements; unary ops and casts with 2 or 4 vectors
-// per lane ran 1-5% slower, f32 -> bf16 of 16M elements 18.7 -> 19.1 / 19.9 us); the rows path keeps 4 items
+// for the flat path on MI355X (6.7 TB/s add at 16M elements; 2 vectors per lane in the 64-lane binary
+// blocks ran slower, 16M f64 == 42.6 -> 44.6 us, and unary ops and casts with 2 or 4 vectors per lane
+// ran 1-5% slower, f32 -> bf16 of 16M elements 18.7 -> 19.1 / 19.9 us); the rows path keeps 4 items
 constexpr int kFlatUnroll = 1;
 constexpr int kUnroll = 4;
 
